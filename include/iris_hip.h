@@ -1,0 +1,171 @@
+/* C ABI of libiris_hip.so: the Iris-3B denoiser forward step on one MI355X (gfx950).
+ *
+ * Conventions shared by every entry point:
+ *  - all pointers are caller-owned device memory; nothing here allocates, frees or
+ *    synchronises the host, and the work is enqueued on `stream` (0 = null stream);
+ *  - return IRIS_OK (0) or a negative IRIS_E_* code; iris_last_error() returns the
+ *    message of the calling thread's last failure. Arguments are validated on the
+ *    host before anything is launched, as the reference wrappers do with ValueError
+ *    (src/iris_metal/kernels.py:299-306);
+ *  - dtype codes: IRIS_F32, IRIS_BF16; FP32 is required where the reference requires it
+ *    (norm gains, rotary tables, modulation vectors, src/iris_metal/kernels.py:20-21);
+ *  - matrices are row-major; "rows" are tokens (or pixels); widths are in elements.
+ *
+ * The reference's kernel-level FFI is torch.mps.compile_shader + getattr(lib, name)(...)
+ * (src/iris_metal/kernels.py:309-311); each entry below names the kernel or the
+ * PyTorch op of the reference forward (src/iris_metal/model.py:177-345) it replaces.
+ */
+#ifndef IRIS_HIP_H
+#define IRIS_HIP_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { IRIS_OK = 0, IRIS_E_INVALID = -1, IRIS_E_LAUNCH = -2, IRIS_E_UNSUPPORTED = -3 };
+enum { IRIS_F32 = 0, IRIS_BF16 = 1 };
+/* GEMM epilogues (bias is a separate optional pointer and is added first). */
+enum { IRIS_EPI_NONE = 0, IRIS_EPI_SILU_MUL = 1 };
+/* Activations of the GEMV input / output. */
+enum { IRIS_ACT_NONE = 0, IRIS_ACT_SILU = 1 };
+
+const char* iris_last_error(void);
+/* Library ABI version (bumped on any signature change). */
+int iris_abi_version(void);
+
+/* rms_norm_modulate (src/iris_metal/kernels.py:116-146, wrapper 413-452):
+ * out[r] = (rmsnorm(x[r]) * weight * (1 + scale[b]) + shift[b]) cast to out_dtype,
+ * b = r / rows_per_batch, shift/scale rows mod_stride floats apart. width % 128 == 0, <= 8192. */
+int iris_rms_norm_modulate(const void* x, int x_dtype, void* out, int out_dtype, const float* weight,
+                           const float* shift, const float* scale, long rows, long rows_per_batch, int width,
+                           long mod_stride, float eps, hipStream_t stream);
+
+/* gated_residual_rms_norm_ (src/iris_metal/kernels.py:148-175, wrapper 455-480):
+ * residual[r] += gate[b] * rmsnorm(branch[r]) * weight, in place on the FP32 residual. */
+int iris_gated_residual_rms_norm(float* residual, const void* branch, int branch_dtype, const float* weight,
+                                 const float* gate, long rows, long rows_per_batch, int width, long mod_stride,
+                                 float eps, hipStream_t stream);
+
+/* qk_norm_rope (src/iris_metal/kernels.py:37-84, wrapper 334-397): per (batch, token, head)
+ * RMSNorm over 128 values with an FP32 gain, then rotation of pairs (2j, 2j+1) by
+ * (cos, sin)[dst_offset + token, j]; reads heads at col_offset of a [batch, n_src, row_stride]
+ * projection and writes [batch, heads, n_dst, 128] rows dst_offset + token.
+ * cos/sin: FP32 [table_rows, 64]. */
+int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int dst_dtype, const float* weight,
+                      const float* cos_table, const float* sin_table, long table_rows, int batch, long n_src,
+                      long n_dst, int heads, long dst_offset, long row_stride, long col_offset, float eps,
+                      hipStream_t stream);
+
+/* The V half of the attention input (src/iris_metal/model.py:243-250 builds [B,Hkv,N,128]):
+ * heads at col_offset of a BF16 [batch, n_src, row_stride] projection are written transposed,
+ * dst[b, h, d, dst_offset + token] in a BF16 [batch, heads, 128, n_dst] buffer. */
+int iris_v_heads_t(const void* src, void* dst, int batch, long n_src, long n_dst, int heads, long dst_offset,
+                   long row_stride, long col_offset, hipStream_t stream);
+
+/* softmax(q k^T * scale) v over a joint sequence of n tokens (F.scaled_dot_product_attention
+ * with GQA, src/iris_metal/model.py:243-250; src/iris3b/nn/attention.py:61-91).
+ * q: BF16 [batch, heads, n_pad, 128]; k: BF16 [batch, kv_heads, n_pad, 128];
+ * vt: BF16 [batch, kv_heads, 128, n_pad] with zeros in columns >= n; n_pad = n rounded up to 64.
+ * Output row r of batch b goes to out0 row (b*out_batch_rows0 + r) when r < n_split, else to out1
+ * row (b*out_batch_rows1 + r - n_split), column h*128 + d, BF16, row stride ld_out; a null out
+ * pointer skips its rows. With gate0/gate1 (rows b*gate_batch_rows{0,1} + r or r - n_split,
+ * stride ld_gate) the stored value is multiplied by sigmoid(gate) (the attention gate of
+ * src/iris_metal/model.py:282-283, 309). */
+int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int heads, int kv_heads, long n,
+                    long n_pad, long n_split, float scale, void* out0, void* out1, long ld_out,
+                    long out_batch_rows0, long out_batch_rows1, const void* gate0, const void* gate1, long ld_gate,
+                    long gate_batch_rows0, long gate_batch_rows1, hipStream_t stream);
+
+/* F.linear on bf16 MFMA (src/iris_metal/model.py:46-52): C[m, n] = sum_k A[m, k] B[n, k] + bias[n]
+ * with A BF16 [m, lda], B (the weight) BF16 [n, ldb], C in c_dtype with row stride ldc.
+ * k % 64 == 0. IRIS_EPI_SILU_MUL: B holds w1 / w3 rows interleaved in 32-row groups
+ * (rows 64p..64p+31 = w1 rows 32p.., rows 64p+32..64p+63 = w3 rows 32p..) and
+ * C[m, j] = silu(a_j) * b_j is n/2 wide (SwiGLU, src/iris3b/nn/mlp.py:24-40). */
+int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n, int k,
+                   long lda, long ldb, long ldc, int epilogue, hipStream_t stream);
+
+/* Tuning hook for the benchmark sweep: force the GEMM tile (0: 256x256, 1: 256x128,
+ * 2: 128x128) or restore the automatic choice (-1). No counterpart in the reference. */
+int iris_gemm_force_tile(int tile);
+
+/* Up to two GEMMs of equal n, k and strides in one launch (the image and text streams of a
+ * dual-stream block, src/iris_metal/model.py:273-289). */
+int iris_gemm_bf16_grouped(int groups, const void* const* a, const void* const* b, const float* const* bias,
+                           void* const* c, const int* m, int c_dtype, int n, int k, long lda, long ldb, long ldc,
+                           int epilogue, hipStream_t stream);
+
+/* Matrix-vector products for the timestep MLP and the shared adaLN cores
+ * (src/iris_metal/model.py:190-192; src/iris3b/nn/modulation.py:258-285):
+ * y[b, n] = act_out(sum_k W[n, k] act_in(x[b, k]) + bias[n]), W BF16 [n, k];
+ * with n_extra > 0, out[j, b, n] = y[b, n] + extra_bias[j, n] for j < n_extra
+ * (the per-block adaLN biases added to a shared core). */
+int iris_gemv_bf16(const void* w, const float* x, int batch, int n, int k, const float* bias,
+                   const float* extra_bias, int n_extra, float* out, int in_act, int out_act, hipStream_t stream);
+
+/* Sinusoidal timestep features [cos | sin] (src/iris3b/nn/embeddings.py:41-45):
+ * out[b, j] = cos(t[b] * freqs[j]), out[b, half + j] = sin(t[b] * freqs[j]). */
+int iris_timestep_features(const float* t, const float* freqs, int batch, int half, float* out,
+                           hipStream_t stream);
+
+/* Patchify + pixel embedding (src/iris_metal/model.py:188-189, 208-210; PixelEmbedder,
+ * src/iris3b/nn/embeddings.py:291-328; pixel_rms_norm, src/iris_metal/kernels.py:217-232):
+ * patches BF16 [batch, L, patch_stride] (first 3*p*p columns) in (channel, row, column) order;
+ * pixels [batch*L, p*p, 16] = x W^T + b + sincos position (pos_x [W, 8], pos_y [H, 8]);
+ * normed BF16 = rmsnorm(pixels) * norm_weight. */
+int iris_patchify_embed(const float* x, int batch, int height, int width, int patch, void* patches,
+                        long patch_stride, const float* pix_w, const float* pix_b, const float* pos_x, const float* pos_y,
+                        const float* norm_weight, float eps, void* pixels, int pixels_dtype, void* normed,
+                        hipStream_t stream);
+
+/* pixel_rms_norm (src/iris_metal/kernels.py:217-232): out = rmsnorm(pixels) * weight, 16 channels. */
+int iris_pixel_rms_norm(const void* pixels, int pixels_dtype, void* out, const float* weight, long n_pixels,
+                        float eps, hipStream_t stream);
+
+/* pixel_mlp_ (src/iris_metal/kernels.py:235-293, wrapper 527-584), per pixel of 16 channels:
+ * x = pixels + branch*(1+scale1)+shift1; h = rmsnorm(x)*norm_weight;
+ * x += (fc2(gelu_erf(fc1(h))))*(1+scale2)+shift2; pixels = x; next_input = rmsnorm(x)*next_norm_weight.
+ * mods BF16 [n_pixels, 64] = (scale1, shift1, scale2, shift2); fc1 [64,16], fc2 [16,64] FP32. */
+int iris_pixel_mlp(void* pixels, int pixels_dtype, const void* branch, const void* mods, const float* norm_weight,
+                   const float* fc1_w, const float* fc1_b, const float* fc2_w, const float* fc2_b,
+                   const float* next_norm_weight, void* next_input, long n_pixels, float eps, hipStream_t stream);
+
+/* Head + unpatchify (src/iris_metal/model.py:214-217): out[b, c, y, x] = h[pixel] . w[c] + bias[c]
+ * for h BF16 [batch*L, p*p, 16] (pixels row-major in each patch), w FP32 [3, 16]. */
+int iris_unpatchify_head(const void* h, const float* w, const float* bias, float* out, int batch, int height,
+                         int width, int patch, hipStream_t stream);
+
+/* s_cond = silu(t_emb + image) (src/iris_metal/model.py:207): out[r] = silu(x[r] + t[r / rows_per_batch]). */
+int iris_silu_add_rows(const float* x, const float* t, long rows, long rows_per_batch, int width, void* out,
+                       int out_dtype, hipStream_t stream);
+
+/* Row-block copy, dst[b*dst_batch_rows + dst_row_offset + r] = src[b*src_batch_rows + src_row_offset + r]
+ * for r < rows: the [text | image] join (src/iris_metal/model.py:201-202) and the image-only
+ * slice of the last block (model.py:307-308). FP32 rows of `width`. */
+int iris_copy_rows(const float* src, float* dst, int batch, long rows, int width, long src_batch_rows,
+                   long src_row_offset, long dst_batch_rows, long dst_row_offset, hipStream_t stream);
+
+/* Turbo flow-Euler update in FP32, in the reference's operation order
+ * (src/iris3b/sampling.py:129-135): clean = x - sigma*v; x_next = (1-sigma_next)*clean
+ * + sigma_next*((x - (1-sigma)*clean)/sigma). x_next may be null (last step). */
+int iris_flow_euler(const float* x, const float* v, long n, float sigma, float sigma_next, float* x_next,
+                    float* clean, hipStream_t stream);
+
+/* First-order DPM-Solver++ step (src/iris3b/flow/solver.py:90-94 with x0 = x - s*v):
+ * x_next = c_x * x - c_x0 * (x - s * v). */
+int iris_dpm1_update(const float* x, const float* v, long n, float s, float c_x, float c_x0, float* x_next,
+                     hipStream_t stream);
+
+/* Classifier-free guidance combine (src/iris3b/flow/solver.py:72-74): out = u + scale*(c - u). */
+int iris_cfg_combine(const float* v_uncond, const float* v_cond, long n, float scale, float* out,
+                     hipStream_t stream);
+
+/* out = clamp(x, lo, hi) (src/iris3b/sampling.py:138). */
+int iris_clamp(const float* x, long n, float lo, float hi, float* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IRIS_HIP_H */

@@ -1,0 +1,293 @@
+// Flash attention (forward, no mask) for 128-wide heads on gfx950 bf16 MFMA, with grouped
+// K/V heads and the attention gate fused into the store.
+//
+// Workgroup = 4 waves sharing one K/V head: with G = heads / kv_heads query heads per K/V
+// head, a workgroup serves hpw = min(G, 4) of them and 64 * 4 / hpw query rows, one wave per
+// (query head, 64-row block). K/V tiles of 64 keys are staged through LDS once and read by
+// all four waves, double-buffered with a register prefetch.
+//
+// Each wave computes S^T = K Q^T (v_mfma_f32_32x32x16_bf16, K fragments from LDS, Q
+// fragments held in registers), so every lane owns one query column and 32 of the 64 keys
+// of the tile: the online-softmax row max / sum need a single cross-lane exchange (lane ^ 32).
+// The probabilities, converted to bf16 in place, are exactly the B operand of O^T = V^T P^T
+// (with a fixed permutation of the keys inside each 16-key step, applied identically to the
+// V^T fragments), so P never leaves registers. V arrives pre-transposed ([d, token]) so that
+// V^T fragments are plain LDS reads.
+#include "iris_common.hpp"
+
+namespace iris {
+namespace {
+
+constexpr int kHd = 128;
+constexpr int kKv = 64;               // keys per tile
+constexpr int kKStride = kHd + 8;     // LDS row of K: 272 bytes (16 lanes -> 64 distinct banks)
+constexpr int kVStride = kKv + 4;     // LDS row of V^T: 136 bytes (32 lanes -> 64 distinct banks)
+constexpr int kKTile = kKv * kKStride;
+constexpr int kVTile = kHd * kVStride;
+
+struct AttnArgs {
+  const bf16* q;
+  const bf16* k;
+  const bf16* vt;
+  bf16* out0;
+  bf16* out1;
+  const bf16* gate0;
+  const bf16* gate1;
+  long ld_out, ld_gate;
+  long out_brows0, out_brows1, gate_brows0, gate_brows1;
+  int heads, kv_heads, n, n_pad, n_split;
+  int hpw, rows_per_wg, n_qblocks, n_hgroups;
+  int total_wg;
+  float scale_log2;
+};
+
+__global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16 k_lds[2 * kKTile];
+  __shared__ __attribute__((aligned(16))) bf16 v_lds[2 * kVTile];
+
+  // logical workgroup: (b, kv head, head group) major, query block minor; the XCD remap keeps
+  // the query blocks of one K/V head on one XCD so its K/V stay in that L2.
+  int wg = xcd_remap(blockIdx.x, p.total_wg);
+  const int qblk = wg % p.n_qblocks;
+  wg /= p.n_qblocks;
+  const int hg = wg % p.n_hgroups;
+  wg /= p.n_hgroups;
+  const int kvh = wg % p.kv_heads;
+  const int b = wg / p.kv_heads;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  const int w = tid >> 6;
+  const int group = p.heads / p.kv_heads;
+  const int h = kvh * group + hg * p.hpw + (w % p.hpw);
+  const int q0 = qblk * p.rows_per_wg + (w / p.hpw) * 64;
+  const long n_pad = p.n_pad;
+
+  // Q fragments: B operand of S^T = K Q^T; lane holds query q0 + qb*32 + l32, dims s*16 + g*8 .. +8
+  const bf16* qh = p.q + (static_cast<long>(b) * p.heads + h) * n_pad * kHd;
+  bf16x8 qf[2][8];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const long row = min(static_cast<long>(q0 + qb * 32 + l32), n_pad - 1);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[qb][s] = *reinterpret_cast<const bf16x8*>(qh + row * kHd + s * 16 + g * 8);
+  }
+
+  const bf16* kh = p.k + (static_cast<long>(b) * p.kv_heads + kvh) * n_pad * kHd;
+  const bf16* vh = p.vt + (static_cast<long>(b) * p.kv_heads + kvh) * kHd * n_pad;
+
+  // per-thread fetch: 4 K chunks (key idx/16, dims 8*(idx%16)) and 4 V^T chunks (dim idx/8, keys 8*(idx%8))
+  bf16x8 kr[4], vr[4];
+  auto fetch = [&](int t) {
+    const long kv0 = static_cast<long>(t) * kKv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      kr[i] = *reinterpret_cast<const bf16x8*>(kh + (kv0 + (idx >> 4)) * kHd + (idx & 15) * 8);
+      vr[i] = *reinterpret_cast<const bf16x8*>(vh + static_cast<long>(idx >> 3) * n_pad + kv0 + (idx & 7) * 8);
+    }
+  };
+  auto stash = [&](int buf) {
+    bf16* kl = k_lds + buf * kKTile;
+    bf16* vl = v_lds + buf * kVTile;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      *reinterpret_cast<bf16x8*>(kl + (idx >> 4) * kKStride + (idx & 15) * 8) = kr[i];
+      // V^T rows are 136 bytes: 8-byte aligned only, so two 8-byte writes
+      bf16* dst = vl + (idx >> 3) * kVStride + (idx & 7) * 8;
+      *reinterpret_cast<bf16x4*>(dst) = bf16x4{vr[i][0], vr[i][1], vr[i][2], vr[i][3]};
+      *reinterpret_cast<bf16x4*>(dst + 4) = bf16x4{vr[i][4], vr[i][5], vr[i][6], vr[i][7]};
+    }
+  };
+
+  f32x16 o[4][2];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db][0] = o[db][1] = f32x16{};
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.0f, 0.0f};
+  const float sl2 = p.scale_log2;
+
+  const int n_tiles = (p.n + kKv - 1) / kKv;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    const int cur = t & 1;
+    if (t + 1 < n_tiles) fetch(t + 1);
+    const bf16* kl = k_lds + cur * kKTile;
+    const bf16* vl = v_lds + cur * kVTile;
+
+    // S^T[key, q] for keys kb*32 + (8 (r/4) + 4 g + r%4), queries qb*32 + l32
+    f32x16 s[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s[kb][0] = s[kb][1] = f32x16{};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      bf16x8 kf[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+        kf[kb] = *reinterpret_cast<const bf16x8*>(kl + (kb * 32 + l32) * kKStride + st * 16 + g * 8);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          s[kb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[qb][st], s[kb][qb], 0, 0, 0);
+    }
+
+    const int kv0 = t * kKv;
+    if (kv0 + kKv > p.n) {  // tail tile: keys >= n do not exist
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= p.n) s[kb][0][r] = s[kb][1][r] = -INFINITY;
+        }
+    }
+
+    // online softmax in the log2 domain, one query column per lane (and its partner lane ^ 32)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run[qb], mx * sl2);
+      const float alpha = exp2f(m_run[qb] - m_new);
+      m_run[qb] = m_new;
+      float sum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = exp2f(s[kb][qb][r] * sl2 - m_new);
+          s[kb][qb][r] = pv;
+          sum += pv;
+        }
+      l_run[qb] = l_run[qb] * alpha + sum;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
+    }
+
+    // O^T[d, q] += V^T[d, keys] P^T[keys, q], 16 keys per MFMA step: k-index g*8 + m is
+    // key kb*32 + 16 jj + 8 (m / 4) + 4 g + m % 4 for both operands.
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        bf16x8 pf[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pf[qb][e] = from_f32<bf16>(s[kb][qb][8 * jj + e]);
+        const int off = kb * 32 + 16 * jj + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const bf16* vrow = vl + (db * 32 + l32) * kVStride + off;
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
+          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 8);
+          const bf16x8 vf = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb], o[db][qb], 0, 0, 0);
+        }
+      }
+    }
+
+    if (t + 1 < n_tiles) stash(cur ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane owns query q0 + qb*32 + l32 and dims db*32 + 8 j + 4 g + (0..3)
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l = l_run[qb] + __shfl_xor(l_run[qb], 32);
+    const float inv = 1.0f / l;
+    const int row = q0 + qb * 32 + l32;
+    if (row >= p.n) continue;
+    const bool first = row < p.n_split;
+    bf16* out = first ? p.out0 : p.out1;
+    const bf16* gate = first ? p.gate0 : p.gate1;
+    const long r = first ? row : row - p.n_split;
+    if (out == nullptr) continue;
+    bf16* orow_ptr = out + (b * (first ? p.out_brows0 : p.out_brows1) + r) * p.ld_out + h * kHd;
+    const bf16* grow_ptr =
+        gate ? gate + (b * (first ? p.gate_brows0 : p.gate_brows1) + r) * p.ld_gate + h * kHd : nullptr;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = db * 32 + 8 * j + 4 * g;
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = o[db][qb][4 * j + e] * inv;
+        if (grow_ptr) {
+          const f32x4 gv = load4(grow_ptr + d0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] *= sigmoid(gv[e]);
+        }
+        store4(orow_ptr + d0, v);
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace iris
+
+using namespace iris;
+
+extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int heads, int kv_heads,
+                               long n, long n_pad, long n_split, float scale, void* out0, void* out1, long ld_out,
+                               long out_batch_rows0, long out_batch_rows1, const void* gate0, const void* gate1,
+                               long ld_gate, long gate_batch_rows0, long gate_batch_rows1, hipStream_t stream) {
+  IRIS_REQUIRE(batch >= 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0,
+               "flash_attn: query heads %d must be a multiple of K/V heads %d", heads, kv_heads);
+  const int group = heads / kv_heads;
+  IRIS_REQUIRE((group & (group - 1)) == 0, "flash_attn: heads per K/V head must be a power of two (got %d)", group);
+  IRIS_REQUIRE(n > 0 && n_pad >= n && n_pad % 64 == 0 && n_pad < (1L << 24),
+               "flash_attn: n_pad must be n rounded up to a multiple of 64");
+  IRIS_REQUIRE(n_split >= 0 && n_split <= n, "flash_attn: n_split outside [0, n]");
+  IRIS_REQUIRE(ld_out >= heads * 128L && ld_out % 4 == 0, "flash_attn: bad ld_out");
+  IRIS_REQUIRE((!gate0 && !gate1) || (ld_gate >= heads * 128L && ld_gate % 4 == 0), "flash_attn: bad ld_gate");
+  IRIS_REQUIRE(out_batch_rows0 >= n_split && out_batch_rows1 >= n - n_split, "flash_attn: output batch stride too small");
+  IRIS_REQUIRE((!gate0 || gate_batch_rows0 >= n_split) && (!gate1 || gate_batch_rows1 >= n - n_split),
+               "flash_attn: gate batch stride too small");
+  IRIS_REQUIRE(q && k && vt, "flash_attn: null input");
+  IRIS_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(vt, 16), "flash_attn: inputs must be 16-byte aligned");
+  if (batch == 0) return IRIS_OK;
+  AttnArgs args{};
+  args.q = static_cast<const bf16*>(q);
+  args.k = static_cast<const bf16*>(k);
+  args.vt = static_cast<const bf16*>(vt);
+  args.out0 = static_cast<bf16*>(out0);
+  args.out1 = static_cast<bf16*>(out1);
+  args.gate0 = static_cast<const bf16*>(gate0);
+  args.gate1 = static_cast<const bf16*>(gate1);
+  args.ld_out = ld_out;
+  args.ld_gate = ld_gate;
+  args.out_brows0 = out_batch_rows0;
+  args.out_brows1 = out_batch_rows1;
+  args.gate_brows0 = gate_batch_rows0;
+  args.gate_brows1 = gate_batch_rows1;
+  args.heads = heads;
+  args.kv_heads = kv_heads;
+  args.n = static_cast<int>(n);
+  args.n_pad = static_cast<int>(n_pad);
+  args.n_split = static_cast<int>(n_split);
+  args.hpw = group < 4 ? group : 4;
+  args.rows_per_wg = 64 * 4 / args.hpw;
+  args.n_qblocks = static_cast<int>((n + args.rows_per_wg - 1) / args.rows_per_wg);
+  args.n_hgroups = group / args.hpw;
+  const long total = static_cast<long>(batch) * kv_heads * args.n_hgroups * args.n_qblocks;
+  IRIS_REQUIRE(total < (1L << 31), "flash_attn: grid too large");
+  args.total_wg = static_cast<int>(total);
+  args.scale_log2 = scale * 1.4426950408889634f;
+  flash_attn_kernel<<<dim3(args.total_wg), 256, 0, stream>>>(args);
+  return check_launch("flash_attn");
+}

@@ -1,0 +1,236 @@
+// Pixel-stage bandwidth kernels: patchify + pixel embedding, the per-pixel RMSNorm, the
+// post-modulated PiT tail (norm, 16 -> 64 -> 16 exact-GELU MLP, both modulated residual
+// adds, next block's norm) and the 16 -> 3 head with unpatchify. One thread per pixel,
+// all math in FP32; BF16 only where the value is stored.
+#include "iris_common.hpp"
+
+namespace iris {
+namespace {
+
+constexpr int kPix = 16;      // pixel channel width of the PiT stage
+constexpr int kHidden = 64;   // PiT MLP hidden width
+
+template <typename TP>
+__global__ __launch_bounds__(256) void patchify_embed_kernel(
+    const float* __restrict__ x, int batch, int height, int width, int patch, bf16* __restrict__ patches,
+    long patch_stride, const float* __restrict__ pix_w, const float* __restrict__ pix_b, const float* __restrict__ pos_x,
+    const float* __restrict__ pos_y, const float* __restrict__ norm_w, float eps, TP* __restrict__ pixels,
+    bf16* __restrict__ normed) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long hw = static_cast<long>(height) * width;
+  if (idx >= batch * hw) return;
+  const int px_x = static_cast<int>(idx % width);
+  const int px_y = static_cast<int>((idx / width) % height);
+  const long b = idx / hw;
+  float v[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) v[c] = x[(b * 3 + c) * hw + static_cast<long>(px_y) * width + px_x];
+  const int wp = width / patch;
+  const long n_patches = static_cast<long>(height / patch) * wp;
+  const long l = static_cast<long>(px_y / patch) * wp + px_x / patch;
+  const int in_patch = (px_y % patch) * patch + (px_x % patch);
+  const int pp = patch * patch;
+  bf16* prow = patches + (b * n_patches + l) * patch_stride + in_patch;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) prow[c * pp] = from_f32<bf16>(v[c]);
+
+  float e[kPix];
+  float ss = 0.0f;
+#pragma unroll
+  for (int ch = 0; ch < kPix; ++ch) {
+    float acc = v[0] * pix_w[ch * 3 + 0] + v[1] * pix_w[ch * 3 + 1] + v[2] * pix_w[ch * 3 + 2] + pix_b[ch];
+    acc += ch < kPix / 2 ? pos_x[px_x * (kPix / 2) + ch] : pos_y[px_y * (kPix / 2) + ch - kPix / 2];
+    e[ch] = acc;
+    ss += acc * acc;
+  }
+  const long q = (b * n_patches + l) * pp + in_patch;
+  store8(pixels + q * kPix, e);
+  store8(pixels + q * kPix + 8, e + 8);
+  const float r = rsqrtf(ss / kPix + eps);
+  float h[kPix];
+#pragma unroll
+  for (int ch = 0; ch < kPix; ++ch) h[ch] = (e[ch] * r) * norm_w[ch];
+  store8(normed + q * kPix, h);
+  store8(normed + q * kPix + 8, h + 8);
+}
+
+template <typename TP>
+__global__ __launch_bounds__(256) void pixel_rms_norm_kernel(const TP* __restrict__ pixels, bf16* __restrict__ out,
+                                                             const float* __restrict__ weight, long n_pixels,
+                                                             float eps) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= n_pixels) return;
+  float v[kPix];
+  load8(pixels + idx * kPix, v);
+  load8(pixels + idx * kPix + 8, v + 8);
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kPix; ++c) ss += v[c] * v[c];
+  const float r = rsqrtf(ss / kPix + eps);
+#pragma unroll
+  for (int c = 0; c < kPix; ++c) v[c] = (v[c] * r) * weight[c];
+  store8(out + idx * kPix, v);
+  store8(out + idx * kPix + 8, v + 8);
+}
+
+// Exact GELU 0.5 a (1 + erf(a / sqrt 2)), written with erfc so that the tail a << 0, where
+// 1 + erf cancels, keeps full relative precision.
+__device__ __forceinline__ float gelu_erf(float a) { return 0.5f * a * erfcf(-a * 0.70710678118654752f); }
+
+template <typename TP>
+__global__ __launch_bounds__(256) void pixel_mlp_kernel(
+    TP* __restrict__ pixels, const bf16* __restrict__ branch, const bf16* __restrict__ mods,
+    const float* __restrict__ norm_w, const float* __restrict__ fc1_w, const float* __restrict__ fc1_b,
+    const float* __restrict__ fc2_w, const float* __restrict__ fc2_b, const float* __restrict__ next_w,
+    bf16* __restrict__ next_input, long n_pixels, float eps) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= n_pixels) return;
+  float m[4 * kPix];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) load8(mods + idx * 4 * kPix + 8 * i, m + 8 * i);
+  float br[kPix], x[kPix];
+  load8(branch + idx * kPix, br);
+  load8(branch + idx * kPix + 8, br + 8);
+  load8(pixels + idx * kPix, x);
+  load8(pixels + idx * kPix + 8, x + 8);
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kPix; ++c) {
+    x[c] = x[c] + (br[c] * (1.0f + m[c]) + m[kPix + c]);  // scale1, shift1
+    ss += x[c] * x[c];
+  }
+  float r = rsqrtf(ss / kPix + eps);
+  float h[kPix], out[kPix];
+#pragma unroll
+  for (int c = 0; c < kPix; ++c) {
+    h[c] = (x[c] * r) * norm_w[c];
+    out[c] = fc2_b[c];
+  }
+  for (int j = 0; j < kHidden; ++j) {
+    float a = fc1_b[j];
+#pragma unroll
+    for (int c = 0; c < kPix; ++c) a += fc1_w[j * kPix + c] * h[c];
+    const float g = gelu_erf(a);
+#pragma unroll
+    for (int c = 0; c < kPix; ++c) out[c] += fc2_w[c * kHidden + j] * g;
+  }
+  ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kPix; ++c) {
+    x[c] = x[c] + (out[c] * (1.0f + m[2 * kPix + c]) + m[3 * kPix + c]);  // scale2, shift2
+    ss += x[c] * x[c];
+  }
+  store8(pixels + idx * kPix, x);
+  store8(pixels + idx * kPix + 8, x + 8);
+  r = rsqrtf(ss / kPix + eps);
+#pragma unroll
+  for (int c = 0; c < kPix; ++c) h[c] = (x[c] * r) * next_w[c];
+  store8(next_input + idx * kPix, h);
+  store8(next_input + idx * kPix + 8, h + 8);
+}
+
+__global__ __launch_bounds__(256) void unpatchify_head_kernel(const bf16* __restrict__ h, const float* __restrict__ w,
+                                                              const float* __restrict__ bias,
+                                                              float* __restrict__ out, int batch, int height,
+                                                              int width, int patch) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long hw = static_cast<long>(height) * width;
+  if (idx >= batch * hw) return;
+  const int px_x = static_cast<int>(idx % width);
+  const int px_y = static_cast<int>((idx / width) % height);
+  const long b = idx / hw;
+  const int wp = width / patch;
+  const long n_patches = static_cast<long>(height / patch) * wp;
+  const long l = static_cast<long>(px_y / patch) * wp + px_x / patch;
+  const long q = (b * n_patches + l) * patch * patch + (px_y % patch) * patch + (px_x % patch);
+  float v[kPix];
+  load8(h + q * kPix, v);
+  load8(h + q * kPix + 8, v + 8);
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int ch = 0; ch < kPix; ++ch) acc += v[ch] * w[c * kPix + ch];
+    out[(b * 3 + c) * hw + static_cast<long>(px_y) * width + px_x] = acc + bias[c];
+  }
+}
+
+inline unsigned blocks_for(long n) { return static_cast<unsigned>((n + 255) / 256); }
+
+}  // namespace
+}  // namespace iris
+
+using namespace iris;
+
+extern "C" int iris_patchify_embed(const float* x, int batch, int height, int width, int patch, void* patches,
+                                   long patch_stride, const float* pix_w, const float* pix_b, const float* pos_x, const float* pos_y,
+                                   const float* norm_weight, float eps, void* pixels, int pixels_dtype,
+                                   void* normed, hipStream_t stream) {
+  IRIS_REQUIRE(pixels_dtype == IRIS_F32 || pixels_dtype == IRIS_BF16, "patchify_embed: unknown dtype");
+  IRIS_REQUIRE(batch >= 0 && patch > 0 && height > 0 && width > 0,
+               "patchify_embed: bad sizes");
+  IRIS_REQUIRE(height % patch == 0 && width % patch == 0, "input %dx%d is not divisible by patch_size %d", height,
+               width, patch);
+  IRIS_REQUIRE(patch_stride >= 3L * patch * patch, "patchify_embed: patch rows shorter than 3*p*p");
+  IRIS_REQUIRE(x && patches && pix_w && pix_b && pos_x && pos_y && norm_weight && pixels && normed,
+               "patchify_embed: null pointer");
+  const long n = static_cast<long>(batch) * height * width;
+  if (n == 0) return IRIS_OK;
+  if (pixels_dtype == IRIS_F32)
+    patchify_embed_kernel<float><<<blocks_for(n), 256, 0, stream>>>(x, batch, height, width, patch, (bf16*)patches, patch_stride,
+                                                                    pix_w, pix_b, pos_x, pos_y, norm_weight, eps,
+                                                                    (float*)pixels, (bf16*)normed);
+  else
+    patchify_embed_kernel<bf16><<<blocks_for(n), 256, 0, stream>>>(x, batch, height, width, patch, (bf16*)patches, patch_stride,
+                                                                   pix_w, pix_b, pos_x, pos_y, norm_weight, eps,
+                                                                   (bf16*)pixels, (bf16*)normed);
+  return check_launch("patchify_embed");
+}
+
+extern "C" int iris_pixel_rms_norm(const void* pixels, int pixels_dtype, void* out, const float* weight,
+                                   long n_pixels, float eps, hipStream_t stream) {
+  IRIS_REQUIRE(pixels_dtype == IRIS_F32 || pixels_dtype == IRIS_BF16, "pixel_rms_norm: unknown dtype");
+  IRIS_REQUIRE(n_pixels >= 0, "pixel_rms_norm: bad size");
+  IRIS_REQUIRE(pixels && out && weight, "pixel_rms_norm: null pointer");
+  if (n_pixels == 0) return IRIS_OK;
+  if (pixels_dtype == IRIS_F32)
+    pixel_rms_norm_kernel<float><<<blocks_for(n_pixels), 256, 0, stream>>>((const float*)pixels, (bf16*)out, weight,
+                                                                           n_pixels, eps);
+  else
+    pixel_rms_norm_kernel<bf16><<<blocks_for(n_pixels), 256, 0, stream>>>((const bf16*)pixels, (bf16*)out, weight,
+                                                                          n_pixels, eps);
+  return check_launch("pixel_rms_norm");
+}
+
+extern "C" int iris_pixel_mlp(void* pixels, int pixels_dtype, const void* branch, const void* mods,
+                              const float* norm_weight, const float* fc1_w, const float* fc1_b, const float* fc2_w,
+                              const float* fc2_b, const float* next_norm_weight, void* next_input, long n_pixels,
+                              float eps, hipStream_t stream) {
+  IRIS_REQUIRE(pixels_dtype == IRIS_F32 || pixels_dtype == IRIS_BF16, "pixel_mlp_: unknown dtype");
+  IRIS_REQUIRE(n_pixels >= 0, "pixel_mlp_: bad size");
+  IRIS_REQUIRE(pixels && branch && mods && norm_weight && fc1_w && fc1_b && fc2_w && fc2_b && next_norm_weight &&
+                   next_input,
+               "pixel_mlp_: null pointer");
+  if (n_pixels == 0) return IRIS_OK;
+  if (pixels_dtype == IRIS_F32)
+    pixel_mlp_kernel<float><<<blocks_for(n_pixels), 256, 0, stream>>>(
+        (float*)pixels, (const bf16*)branch, (const bf16*)mods, norm_weight, fc1_w, fc1_b, fc2_w, fc2_b,
+        next_norm_weight, (bf16*)next_input, n_pixels, eps);
+  else
+    pixel_mlp_kernel<bf16><<<blocks_for(n_pixels), 256, 0, stream>>>(
+        (bf16*)pixels, (const bf16*)branch, (const bf16*)mods, norm_weight, fc1_w, fc1_b, fc2_w, fc2_b,
+        next_norm_weight, (bf16*)next_input, n_pixels, eps);
+  return check_launch("pixel_mlp");
+}
+
+extern "C" int iris_unpatchify_head(const void* h, const float* w, const float* bias, float* out, int batch,
+                                    int height, int width, int patch, hipStream_t stream) {
+  IRIS_REQUIRE(batch >= 0 && patch > 0 && height > 0 && width > 0 && height % patch == 0 && width % patch == 0,
+               "unpatchify_head: bad sizes");
+  IRIS_REQUIRE(h && w && bias && out, "unpatchify_head: null pointer");
+  const long n = static_cast<long>(batch) * height * width;
+  if (n == 0) return IRIS_OK;
+  unpatchify_head_kernel<<<blocks_for(n), 256, 0, stream>>>((const bf16*)h, w, bias, out, batch, height, width,
+                                                            patch);
+  return check_launch("unpatchify_head");
+}

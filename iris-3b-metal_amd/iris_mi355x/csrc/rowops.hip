@@ -1,0 +1,365 @@
+// Row-wise bandwidth kernels of the trunk: RMSNorm + adaLN modulate, post-norm gated
+// residual, per-head qk-RMSNorm + 2-D RoPE, the V-head transpose, and small row utilities.
+//
+// Layout: one 64-lane wave per row (token) for the D-wide row kernels, 16-byte vector
+// loads, the row cached in registers between the statistics pass and the output pass
+// so HBM sees each byte once.
+#include "iris_common.hpp"
+
+namespace iris {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // 4 waves = 4 rows per 256-thread workgroup
+
+// NV = number of 4-element vectors each lane holds (width <= NV * 256).
+template <int NV, typename TI, typename TO>
+__global__ __launch_bounds__(256) void rms_norm_modulate_kernel(const TI* __restrict__ x, TO* __restrict__ out,
+                                                                const float* __restrict__ weight,
+                                                                const float* __restrict__ shift,
+                                                                const float* __restrict__ scale, long rows,
+                                                                long rows_per_batch, int width, long mod_stride,
+                                                                float eps) {
+  const long row = static_cast<long>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int nv = width >> 2;
+  const TI* xr = x + row * width;
+  f32x4 v[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nv) {
+      v[i] = load4(xr + 4 * j);
+      ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+    }
+  }
+  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
+  const long b = row / rows_per_batch;
+  const float* sh = shift + b * mod_stride;
+  const float* sc = scale + b * mod_stride;
+  TO* o = out + row * width;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nv) {
+      const f32x4 w = load4(weight + 4 * j);
+      const f32x4 s1 = load4(sc + 4 * j);
+      const f32x4 s0 = load4(sh + 4 * j);
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float h = (v[i][e] * r) * w[e];
+        y[e] = h * (1.0f + s1[e]) + s0[e];
+      }
+      store4(o + 4 * j, y);
+    }
+  }
+}
+
+template <int NV, typename TB>
+__global__ __launch_bounds__(256) void gated_residual_kernel(float* __restrict__ residual,
+                                                             const TB* __restrict__ branch,
+                                                             const float* __restrict__ weight,
+                                                             const float* __restrict__ gate, long rows,
+                                                             long rows_per_batch, int width, long mod_stride,
+                                                             float eps) {
+  const long row = static_cast<long>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int nv = width >> 2;
+  const TB* br = branch + row * width;
+  f32x4 v[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nv) {
+      v[i] = load4(br + 4 * j);
+      ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+    }
+  }
+  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
+  const float* g = gate + (row / rows_per_batch) * mod_stride;
+  float* res = residual + row * width;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nv) {
+      const f32x4 w = load4(weight + 4 * j);
+      const f32x4 gv = load4(g + 4 * j);
+      f32x4 acc = load4(res + 4 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += gv[e] * ((v[i][e] * r) * w[e]);
+      store4(res + 4 * j, acc);
+    }
+  }
+}
+
+// 16 lanes per (token, head) row of 128 values; lane s owns elements [8s, 8s+8) = rotary
+// pairs 4s..4s+3. Four rows per wave, sixteen per workgroup.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict__ src, TO* __restrict__ dst,
+                                                           const float* __restrict__ weight,
+                                                           const float* __restrict__ cos_table,
+                                                           const float* __restrict__ sin_table, long n_src,
+                                                           long n_dst, int heads, long dst_offset, long row_stride,
+                                                           long col_offset, float eps) {
+  const long row = static_cast<long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const long b = blockIdx.y;
+  if (row >= n_src * heads) return;  // whole 16-lane groups leave together
+  const long token = row / heads;
+  const int head = static_cast<int>(row - token * heads);
+  float a[8];
+  load8(src + (b * n_src + token) * row_stride + col_offset + head * 128 + 8 * sub, a);
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += a[e] * a[e];
+  const float r = rsqrtf(group_sum<16>(ss) / 128.0f + eps);
+  float w[8];
+  load8(weight + 8 * sub, w);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = (a[e] * r) * w[e];
+  const long out_token = dst_offset + token;
+  const f32x4 c = load4(cos_table + out_token * 64 + 4 * sub);
+  const f32x4 s = load4(sin_table + out_token * 64 + 4 * sub);
+  float y[8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    y[2 * p] = a[2 * p] * c[p] - a[2 * p + 1] * s[p];
+    y[2 * p + 1] = a[2 * p] * s[p] + a[2 * p + 1] * c[p];
+  }
+  store8(dst + ((b * heads + head) * n_dst + out_token) * 128 + 8 * sub, y);
+}
+
+// Transpose 64 tokens x 128 dims of one head into dst[b, h, d, token]. LDS rows are padded
+// by 8 elements (272 bytes) so the column reads of the second phase spread over the banks.
+__global__ __launch_bounds__(256) void v_heads_t_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst,
+                                                        long n_src, long n_dst, int heads, long dst_offset,
+                                                        long row_stride, long col_offset) {
+  __shared__ bf16 tile[64][136];
+  const long t0 = static_cast<long>(blockIdx.x) * 64;
+  const int head = blockIdx.y;
+  const long b = blockIdx.z;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i;  // 64 tokens x 16 chunks of 8
+    const int tok = idx >> 4;
+    const int c = idx & 15;
+    bf16x8 v = {};
+    if (t0 + tok < n_src)
+      v = *reinterpret_cast<const bf16x8*>(src + (b * n_src + t0 + tok) * row_stride + col_offset + head * 128 +
+                                           8 * c);
+    *reinterpret_cast<bf16x8*>(&tile[tok][8 * c]) = v;
+  }
+  __syncthreads();
+  bf16* out = dst + (b * heads + head) * 128 * n_dst + dst_offset + t0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i;  // 128 dims x 8 chunks of 8 tokens
+    const int d = idx >> 3;
+    const int c = idx & 7;
+    if (t0 + 8 * c >= n_src) continue;
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = tile[8 * c + e][d];
+    bf16* o = out + static_cast<long>(d) * n_dst + 8 * c;
+    if (t0 + 8 * c + 8 <= n_src && ((dst_offset + t0) & 7) == 0 && (n_dst & 7) == 0) {
+      *reinterpret_cast<bf16x8*>(o) = v;
+    } else {
+      for (int e = 0; e < 8 && t0 + 8 * c + e < n_src; ++e) o[e] = v[e];
+    }
+  }
+}
+
+template <typename TO>
+__global__ __launch_bounds__(256) void silu_add_rows_kernel(const float* __restrict__ x, const float* __restrict__ t,
+                                                            long rows, long rows_per_batch, int width,
+                                                            TO* __restrict__ out) {
+  const long i4 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long nv = static_cast<long>(width) >> 2;
+  if (i4 >= rows * nv) return;
+  const long row = i4 / nv;
+  const long col = (i4 - row * nv) * 4;
+  const f32x4 a = load4(x + row * width + col);
+  const f32x4 b = load4(t + (row / rows_per_batch) * width + col);
+  f32x4 y;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = silu(a[e] + b[e]);
+  store4(out + row * width + col, y);
+}
+
+__global__ __launch_bounds__(256) void copy_rows_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                        long rows, int width, long src_batch_rows,
+                                                        long src_row_offset, long dst_batch_rows,
+                                                        long dst_row_offset) {
+  const long i4 = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long nv = static_cast<long>(width) >> 2;
+  if (i4 >= rows * nv) return;
+  const long b = blockIdx.y;
+  const long row = i4 / nv;
+  const long col = (i4 - row * nv) * 4;
+  store4(dst + (b * dst_batch_rows + dst_row_offset + row) * width + col,
+         load4(src + (b * src_batch_rows + src_row_offset + row) * width + col));
+}
+
+int nv_bucket(int width) {
+  const int need = (width / 4 + kWave - 1) / kWave;
+  if (need <= 1) return 1;
+  if (need <= 2) return 2;
+  if (need <= 4) return 4;
+  if (need <= 8) return 8;
+  if (need <= 10) return 10;
+  if (need <= 16) return 16;
+  return 32;
+}
+
+#define IRIS_NV_DISPATCH(NVV, ...)              \
+  switch (NVV) {                                \
+    case 1: { constexpr int NV = 1; __VA_ARGS__; } break;   \
+    case 2: { constexpr int NV = 2; __VA_ARGS__; } break;   \
+    case 4: { constexpr int NV = 4; __VA_ARGS__; } break;   \
+    case 8: { constexpr int NV = 8; __VA_ARGS__; } break;   \
+    case 10: { constexpr int NV = 10; __VA_ARGS__; } break; \
+    case 16: { constexpr int NV = 16; __VA_ARGS__; } break; \
+    default: { constexpr int NV = 32; __VA_ARGS__; } break; \
+  }
+
+bool valid_dtype(int dt) { return dt == IRIS_F32 || dt == IRIS_BF16; }
+
+}  // namespace
+}  // namespace iris
+
+using namespace iris;
+
+extern "C" int iris_rms_norm_modulate(const void* x, int x_dtype, void* out, int out_dtype, const float* weight,
+                                      const float* shift, const float* scale, long rows, long rows_per_batch,
+                                      int width, long mod_stride, float eps, hipStream_t stream) {
+  IRIS_REQUIRE(valid_dtype(x_dtype) && valid_dtype(out_dtype), "rms_norm_modulate: unknown dtype");
+  IRIS_REQUIRE(width > 0 && width % 128 == 0 && width <= 8192,
+               "rms_norm_modulate needs a contiguous input, width %% 128 == 0 and <= 8192 (got %d)", width);
+  IRIS_REQUIRE(rows >= 0 && rows_per_batch > 0, "rms_norm_modulate: bad row counts");
+  IRIS_REQUIRE(mod_stride % 4 == 0 && aligned(shift, 16) && aligned(scale, 16) && aligned(weight, 16),
+               "rms_norm_modulate: modulation rows must be 16-byte aligned (mod_stride %% 4 == 0)");
+  IRIS_REQUIRE(x && out && weight && shift && scale, "rms_norm_modulate: null pointer");
+  if (rows == 0) return IRIS_OK;
+  const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  IRIS_NV_DISPATCH(nv_bucket(width), {
+    if (x_dtype == IRIS_F32 && out_dtype == IRIS_BF16)
+      rms_norm_modulate_kernel<NV, float, bf16><<<grid, 256, 0, stream>>>(
+          (const float*)x, (bf16*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
+    else if (x_dtype == IRIS_F32 && out_dtype == IRIS_F32)
+      rms_norm_modulate_kernel<NV, float, float><<<grid, 256, 0, stream>>>(
+          (const float*)x, (float*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
+    else if (x_dtype == IRIS_BF16 && out_dtype == IRIS_BF16)
+      rms_norm_modulate_kernel<NV, bf16, bf16><<<grid, 256, 0, stream>>>(
+          (const bf16*)x, (bf16*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
+    else
+      rms_norm_modulate_kernel<NV, bf16, float><<<grid, 256, 0, stream>>>(
+          (const bf16*)x, (float*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
+  })
+  return check_launch("rms_norm_modulate");
+}
+
+extern "C" int iris_gated_residual_rms_norm(float* residual, const void* branch, int branch_dtype,
+                                            const float* weight, const float* gate, long rows, long rows_per_batch,
+                                            int width, long mod_stride, float eps, hipStream_t stream) {
+  IRIS_REQUIRE(valid_dtype(branch_dtype), "gated_residual_rms_norm: unknown dtype");
+  IRIS_REQUIRE(width > 0 && width % 128 == 0 && width <= 8192,
+               "gated_residual_rms_norm_ shape mismatch: width %% 128 == 0 and <= 8192 (got %d)", width);
+  IRIS_REQUIRE(rows >= 0 && rows_per_batch > 0, "gated_residual_rms_norm: bad row counts");
+  IRIS_REQUIRE(mod_stride % 4 == 0 && aligned(gate, 16) && aligned(weight, 16),
+               "gated_residual_rms_norm: gate rows must be 16-byte aligned");
+  IRIS_REQUIRE(residual && branch && weight && gate, "gated_residual_rms_norm: null pointer");
+  if (rows == 0) return IRIS_OK;
+  const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  IRIS_NV_DISPATCH(nv_bucket(width), {
+    if (branch_dtype == IRIS_BF16)
+      gated_residual_kernel<NV, bf16><<<grid, 256, 0, stream>>>(residual, (const bf16*)branch, weight, gate, rows,
+                                                                rows_per_batch, width, mod_stride, eps);
+    else
+      gated_residual_kernel<NV, float><<<grid, 256, 0, stream>>>(residual, (const float*)branch, weight, gate,
+                                                                 rows, rows_per_batch, width, mod_stride, eps);
+  })
+  return check_launch("gated_residual_rms_norm");
+}
+
+extern "C" int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int dst_dtype, const float* weight,
+                                 const float* cos_table, const float* sin_table, long table_rows, int batch,
+                                 long n_src, long n_dst, int heads, long dst_offset, long row_stride,
+                                 long col_offset, float eps, hipStream_t stream) {
+  IRIS_REQUIRE(valid_dtype(src_dtype) && valid_dtype(dst_dtype), "qk_norm_rope: unknown dtype");
+  IRIS_REQUIRE(heads > 0 && col_offset >= 0 && dst_offset >= 0, "heads must be positive and offsets nonnegative");
+  IRIS_REQUIRE(batch >= 0 && n_src >= 0, "qk_norm_rope: bad sizes");
+  IRIS_REQUIRE(col_offset + heads * 128L <= row_stride,
+               "qk_norm_rope needs a contiguous [B, N, W] input holding the heads");
+  IRIS_REQUIRE(dst_offset + n_src <= table_rows && dst_offset + n_src <= n_dst,
+               "qk_norm_rope rotary tables or output do not cover the written rows");
+  IRIS_REQUIRE(row_stride % 8 == 0 && col_offset % 8 == 0, "qk_norm_rope: rows must be 16-byte aligned");
+  IRIS_REQUIRE(src && dst && weight && cos_table && sin_table, "qk_norm_rope: null pointer");
+  if (batch == 0 || n_src == 0) return IRIS_OK;
+  const dim3 grid(static_cast<unsigned>((n_src * heads + 15) / 16), static_cast<unsigned>(batch));
+#define IRIS_QK_LAUNCH(TI, TO)                                                                                   \
+  qk_norm_rope_kernel<TI, TO><<<grid, 256, 0, stream>>>((const TI*)src, (TO*)dst, weight, cos_table, sin_table, \
+                                                        n_src, n_dst, heads, dst_offset, row_stride, col_offset, \
+                                                        eps)
+  if (src_dtype == IRIS_BF16 && dst_dtype == IRIS_BF16)
+    IRIS_QK_LAUNCH(bf16, bf16);
+  else if (src_dtype == IRIS_BF16)
+    IRIS_QK_LAUNCH(bf16, float);
+  else if (dst_dtype == IRIS_BF16)
+    IRIS_QK_LAUNCH(float, bf16);
+  else
+    IRIS_QK_LAUNCH(float, float);
+#undef IRIS_QK_LAUNCH
+  return check_launch("qk_norm_rope");
+}
+
+extern "C" int iris_v_heads_t(const void* src, void* dst, int batch, long n_src, long n_dst, int heads,
+                              long dst_offset, long row_stride, long col_offset, hipStream_t stream) {
+  IRIS_REQUIRE(heads > 0 && heads <= 65535 && batch >= 0 && batch <= 65535 && n_src >= 0,
+               "v_heads_t: bad sizes");
+  IRIS_REQUIRE(col_offset >= 0 && col_offset + heads * 128L <= row_stride && row_stride % 8 == 0 &&
+                   col_offset % 8 == 0,
+               "v_heads_t: heads must lie in 16-byte aligned rows of the projection");
+  IRIS_REQUIRE(dst_offset >= 0 && dst_offset + n_src <= n_dst, "v_heads_t: output does not cover the rows");
+  IRIS_REQUIRE(src && dst, "v_heads_t: null pointer");
+  if (batch == 0 || n_src == 0) return IRIS_OK;
+  const dim3 grid(static_cast<unsigned>((n_src + 63) / 64), static_cast<unsigned>(heads),
+                  static_cast<unsigned>(batch));
+  v_heads_t_kernel<<<grid, 256, 0, stream>>>((const bf16*)src, (bf16*)dst, n_src, n_dst, heads, dst_offset,
+                                             row_stride, col_offset);
+  return check_launch("v_heads_t");
+}
+
+extern "C" int iris_silu_add_rows(const float* x, const float* t, long rows, long rows_per_batch, int width,
+                                  void* out, int out_dtype, hipStream_t stream) {
+  IRIS_REQUIRE(valid_dtype(out_dtype), "silu_add_rows: unknown dtype");
+  IRIS_REQUIRE(width > 0 && width % 4 == 0 && rows >= 0 && rows_per_batch > 0, "silu_add_rows: bad sizes");
+  IRIS_REQUIRE(x && t && out, "silu_add_rows: null pointer");
+  if (rows == 0) return IRIS_OK;
+  const long n4 = rows * (width / 4);
+  const dim3 grid(static_cast<unsigned>((n4 + 255) / 256));
+  if (out_dtype == IRIS_BF16)
+    silu_add_rows_kernel<bf16><<<grid, 256, 0, stream>>>(x, t, rows, rows_per_batch, width, (bf16*)out);
+  else
+    silu_add_rows_kernel<float><<<grid, 256, 0, stream>>>(x, t, rows, rows_per_batch, width, (float*)out);
+  return check_launch("silu_add_rows");
+}
+
+extern "C" int iris_copy_rows(const float* src, float* dst, int batch, long rows, int width, long src_batch_rows,
+                              long src_row_offset, long dst_batch_rows, long dst_row_offset, hipStream_t stream) {
+  IRIS_REQUIRE(width > 0 && width % 4 == 0 && rows >= 0 && batch >= 0 && batch <= 65535, "copy_rows: bad sizes");
+  IRIS_REQUIRE(src_row_offset >= 0 && dst_row_offset >= 0 && src_row_offset + rows <= src_batch_rows &&
+                   dst_row_offset + rows <= dst_batch_rows,
+               "copy_rows: row block outside its batch");
+  IRIS_REQUIRE(src && dst, "copy_rows: null pointer");
+  if (rows == 0 || batch == 0) return IRIS_OK;
+  const long n4 = rows * (width / 4);
+  const dim3 grid(static_cast<unsigned>((n4 + 255) / 256), static_cast<unsigned>(batch));
+  copy_rows_kernel<<<grid, 256, 0, stream>>>(src, dst, rows, width, src_batch_rows, src_row_offset, dst_batch_rows,
+                                             dst_row_offset);
+  return check_launch("copy_rows");
+}

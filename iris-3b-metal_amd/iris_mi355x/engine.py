@@ -1,0 +1,425 @@
+"""``HipIris``: the Iris-3B velocity predictor ``(x, t, text) -> v`` on one MI355X.
+
+Drop-in for the reference engine's call surface (``MetalIris``, src/iris_metal/model.py:113-217):
+same constructor checks, ``__call__(x, t, text)`` with ``x`` ``[B, 3, H, W]``, model time
+``t`` ``[B]`` and prepared text tokens ``[B, T, D]``, returning FP32 velocity, under no-grad,
+without modifying its inputs. Every operation of the forward is one of the HIP kernels of
+``libiris_hip.so``; torch only provides device memory and the stream.
+
+Precision plan: residual streams (trunk and pixel stage), norm statistics, modulation,
+rotary math and softmax are FP32; GEMM and attention operands are BF16 with FP32
+accumulation; every activation crossing a GEMM is stored BF16 once.
+
+Data layout in HBM (per call shape, allocated once and reused):
+- dual-stream phase: image ``X`` ``[B*L, D]`` and text ``Y`` ``[B*T, D]`` FP32 residuals;
+- single-stream phase: ``tok`` ``[B*N, D]`` FP32 with the text rows first in each batch;
+- packed projections ``[rows, 6400]`` = ``q | k | v | gate`` (one GEMM per stream and block);
+- attention inputs ``q`` ``[B, 20, N_pad, 128]``, ``k`` ``[B, 5, N_pad, 128]``, ``v^T`` ``[B, 5, 128, N_pad]``;
+- pixel stream ``[B*L, p*p, 16]`` FP32 and its BF16 normed copy, adaLN mods ``[B*L, p*p, 64]`` BF16.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels as K
+from . import tables
+from .config import ModelConfig
+
+HEAD_DIM = K.HEAD_DIM
+
+
+def check_supported(cfg: ModelConfig) -> None:
+    """Reject topologies the fused forward does not handle (src/iris_metal/model.py:68-93)."""
+    requirements = {
+        "a pixel stage with post-modulated blocks": cfg.pixel.enabled and cfg.pixel.modulation == "post",
+        "shared_bias modulation with a dual-stream prefix": cfg.modulation == "shared_bias" and cfg.dual_depth > 0,
+        "a single-stream final block": cfg.block_kind(cfg.depth - 1) == "single_stream"
+        and cfg.block == "single_stream",
+        "grouped-query, gated, sandwich-normed, QK-normed attention": (
+            cfg.num_kv_heads is not None
+            and cfg.num_kv_heads < cfg.num_heads
+            and cfg.gated_attention
+            and cfg.sandwich_norm
+            and cfg.qk_norm
+        ),
+        f"{HEAD_DIM}-wide attention heads": (
+            cfg.hidden_size // cfg.num_heads == HEAD_DIM
+            and cfg.pixel.attn_hidden_size // cfg.pixel.num_heads == HEAD_DIM
+        ),
+        "a masked text adapter with text RoPE and position table": (
+            cfg.text_adapter != "linear" and cfg.text_rope and cfg.text_abs_pos_embed
+        ),
+        "16-channel pixels with a 64-wide MLP": cfg.pixel.hidden_size == K.PIXEL_WIDTH
+        and int(cfg.pixel.hidden_size * cfg.pixel.mlp_ratio) == K.PIXEL_HIDDEN and cfg.in_channels == 3,
+    }
+    missing = [name for name, ok in requirements.items() if not ok]
+    if missing:
+        raise ValueError(f"HipIris supports the released Iris-3B topology; this model lacks {missing}")
+
+
+def require_finite(result: torch.Tensor) -> torch.Tensor:
+    """Raise rather than return an overflowed result (src/iris_metal/model.py:102-110)."""
+    if not torch.isfinite(result).all():
+        raise FloatingPointError("the model produced non-finite values; please report the input and settings")
+    return result
+
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+@dataclass
+class _Shape:
+    batch: int
+    height: int
+    width: int
+    n_text: int
+
+
+class HipIris:
+    """Velocity predictor over a ``state_dict`` with the reference's key names.
+
+    ``HipIris(cfg, state_dict)`` or ``HipIris.from_module(dit)`` for an object exposing ``cfg``
+    and ``state_dict()`` (an upstream ``IrisDiT``).
+    """
+
+    def __init__(self, cfg: ModelConfig, state_dict: dict[str, torch.Tensor], device: str | torch.device = "cuda"):
+        cfg.validate()
+        check_supported(cfg)
+        self.cfg = cfg
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("HipIris runs on the GPU only")
+        self.eps = cfg.norm_eps
+        self.hidden_pad = _round_up(cfg.mlp_hidden, 64)
+        self._prepare(state_dict)
+        self._ws: dict | None = None
+        self._ws_shape: _Shape | None = None
+        self._tables: dict = {}
+
+    @classmethod
+    def from_module(cls, dit, device: str | torch.device = "cuda") -> "HipIris":
+        return cls(dit.cfg, dit.state_dict(), device)
+
+    # -- weights ----------------------------------------------------------------------
+    def _prepare(self, sd: dict[str, torch.Tensor]) -> None:
+        cfg, dev = self.cfg, self.device
+
+        def f32(name: str) -> torch.Tensor:
+            return sd[name].detach().to(dev, torch.float32).contiguous()
+
+        def bf(t: torch.Tensor) -> torch.Tensor:
+            return t.detach().to(dev, torch.bfloat16).contiguous()
+
+        def w(name: str) -> torch.Tensor:
+            return bf(sd[f"{name}.weight"])
+
+        def cat_rows(*names: str) -> torch.Tensor:
+            return bf(torch.cat([sd[f"{n}.weight"].detach().float() for n in names], dim=0))
+
+        def swiglu(prefix: str) -> tuple[torch.Tensor, torch.Tensor]:
+            w1 = sd[f"{prefix}.w1.weight"].detach().float()
+            w3 = sd[f"{prefix}.w3.weight"].detach().float()
+            w2 = sd[f"{prefix}.w2.weight"].detach().float()
+            packed = K.pack_swiglu(w1, w3, self.hidden_pad)
+            w2p = torch.zeros(w2.shape[0], self.hidden_pad)
+            w2p[:, : w2.shape[1]] = w2
+            return bf(packed), bf(w2p)
+
+        # the patch embedder's K (3*p*p) is zero-padded to the GEMM's multiple of 64
+        s_w = sd["s_embedder.proj.weight"].detach().float()
+        self.patch_k = _round_up(s_w.shape[1], 64)
+        self.s_w = bf(torch.nn.functional.pad(s_w, (0, self.patch_k - s_w.shape[1])))
+        self.s_b = f32("s_embedder.proj.bias")
+        self.t0_w, self.t0_b = w("t_embedder.mlp.0"), f32("t_embedder.mlp.0.bias")
+        self.t2_w, self.t2_b = w("t_embedder.mlp.2"), f32("t_embedder.mlp.2.bias")
+        self.core_img_w, self.core_img_b = w("modulation_cores.adaln_img"), f32("modulation_cores.adaln_img.bias")
+        self.core_txt_w, self.core_txt_b = w("modulation_cores.adaln_txt"), f32("modulation_cores.adaln_txt.bias")
+
+        img_bias, txt_bias = [], []
+        self.blocks = []
+        for i in range(cfg.depth):
+            b = f"blocks.{i}"
+            if cfg.block_kind(i) == "mmdit":
+                blk = {"kind": "mmdit", "img_mod": len(img_bias), "txt_mod": len(txt_bias)}
+                img_bias.append(f32(f"{b}.adaln_img.bias"))
+                txt_bias.append(f32(f"{b}.adaln_txt.bias"))
+                for st in ("x", "y"):
+                    blk[f"qkvg_{st}"] = cat_rows(f"{b}.attn.q_proj_{st}", f"{b}.attn.k_proj_{st}",
+                                                 f"{b}.attn.v_proj_{st}", f"{b}.attn_gate_{st}")
+                    blk[f"proj_{st}_w"], blk[f"proj_{st}_b"] = w(f"{b}.attn.proj_{st}"), f32(f"{b}.attn.proj_{st}.bias")
+                    blk[f"w13_{st}"], blk[f"w2_{st}"] = swiglu(f"{b}.mlp_{st}")
+                    for nm in (f"norm_{st}1", f"norm_{st}2", f"attn_post_norm_{st}", f"mlp_post_norm_{st}"):
+                        blk[nm] = f32(f"{b}.{nm}.weight")
+                    for nm in (f"q_norm_{st}", f"k_norm_{st}"):
+                        blk[nm] = f32(f"{b}.attn.{nm}.weight")
+            else:
+                blk = {"kind": "single", "img_mod": len(img_bias)}
+                img_bias.append(f32(f"{b}.adaln.bias"))
+                blk["qkvg"] = cat_rows(f"{b}.q_proj", f"{b}.k_proj", f"{b}.v_proj", f"{b}.attn_gate")
+                blk["proj_w"], blk["proj_b"] = w(f"{b}.attn_proj"), f32(f"{b}.attn_proj.bias")
+                blk["w13"], blk["w2"] = swiglu(f"{b}.mlp")
+                for nm in ("norm1", "norm2", "attn_post_norm", "mlp_post_norm", "q_norm", "k_norm"):
+                    blk[nm] = f32(f"{b}.{nm}.weight")
+            self.blocks.append(blk)
+        self.img_bias = torch.stack(img_bias).contiguous()
+        self.txt_bias = torch.stack(txt_bias).contiguous()
+
+        self.pix_w, self.pix_b = f32("pixel_embedder.proj.weight"), f32("pixel_embedder.proj.bias")
+        self.pixel_blocks = []
+        for j in range(cfg.pixel.depth):
+            b = f"pixel_blocks.{j}"
+            self.pixel_blocks.append({
+                "norm1": f32(f"{b}.norm1.weight"), "norm2": f32(f"{b}.norm2.weight"),
+                "adaln_w": w(f"{b}.adaln"), "adaln_b": f32(f"{b}.adaln.bias"),
+                "compress_w": w(f"{b}.compress"), "compress_b": f32(f"{b}.compress.bias"),
+                "qkv_w": w(f"{b}.attn.qkv"),
+                "q_norm": f32(f"{b}.attn.q_norm.weight"), "k_norm": f32(f"{b}.attn.k_norm.weight"),
+                "proj_w": w(f"{b}.attn.proj"), "proj_b": f32(f"{b}.attn.proj.bias"),
+                "expand_w": w(f"{b}.expand"), "expand_b": f32(f"{b}.expand.bias"),
+                "fc1_w": f32(f"{b}.mlp.fc1.weight"), "fc1_b": f32(f"{b}.mlp.fc1.bias"),
+                "fc2_w": f32(f"{b}.mlp.fc2.weight"), "fc2_b": f32(f"{b}.mlp.fc2.bias"),
+            })
+        self.final_norm = f32("final_layer.norm.weight")
+        self.final_w, self.final_b = f32("final_layer.linear.weight"), f32("final_layer.linear.bias")
+        self.t_freqs = tables.timestep_freqs(256, cfg.timestep_max_period, self.device)
+        if "t_embedder.mlp.0.weight" in sd and sd["t_embedder.mlp.0.weight"].shape[1] != 256:
+            raise ValueError("HipIris expects 256 timestep frequencies")
+
+    # -- per-shape state ----------------------------------------------------------------
+    def _workspace(self, shape: _Shape) -> dict:
+        if self._ws is not None and self._ws_shape == shape:
+            return self._ws
+        self._ws = None
+        cfg, dev = self.cfg, self.device
+        B, T = shape.batch, shape.n_text
+        p = cfg.patch_size
+        hp, wp = shape.height // p, shape.width // p
+        Lp = hp * wp
+        N = T + Lp
+        D = cfg.hidden_size
+        H, Hkv = cfg.num_heads, cfg.kv_heads
+        n_pad = _round_up(N, 64)
+        l_pad = _round_up(Lp, 64)
+        pp = p * p
+        px = cfg.pixel
+        qkvg_w = (H + 2 * Hkv) * HEAD_DIM + D
+        bf16, f32 = torch.bfloat16, torch.float32
+
+        def e(*s, dtype=bf16):
+            return torch.empty(*s, device=dev, dtype=dtype)
+
+        n_img, n_txt = self.img_bias.shape[0], self.txt_bias.shape[0]
+        ws = {
+            "L": Lp, "N": N, "n_pad": n_pad, "l_pad": l_pad, "grid": (hp, wp),
+            "patches": torch.zeros(B * Lp, self.patch_k, device=dev, dtype=bf16),
+            "X": e(B * Lp, D, dtype=f32), "Y": e(B * T, D, dtype=f32), "tok": e(B * N, D, dtype=f32),
+            "tfeat": e(B, 256, dtype=f32), "th": e(B, D, dtype=f32), "temb": e(B, D, dtype=f32),
+            "mods_img": e(n_img, B, 6 * D, dtype=f32), "mods_txt": e(n_txt, B, 6 * D, dtype=f32),
+            "h_tok": e(B * N, D), "qkvg": e(B * N, qkvg_w), "attn": e(B * N, D), "branch": e(B * N, D),
+            "hh": e(B * N, self.hidden_pad),
+            "q": e(B, H, n_pad, HEAD_DIM), "k": e(B, Hkv, n_pad, HEAD_DIM),
+            "vt": torch.zeros(B, Hkv, HEAD_DIM, n_pad, device=dev, dtype=bf16),
+            "scond": e(B * Lp, D),
+            "pixels": e(B * Lp, pp, K.PIXEL_WIDTH, dtype=f32), "hpix": e(B * Lp, pp, K.PIXEL_WIDTH),
+            "mods_pix": e(B * Lp, pp, 4 * K.PIXEL_WIDTH),
+            "cp": e(B * Lp, px.attn_hidden_size), "pq": e(B * Lp, 3 * px.attn_hidden_size),
+            "pa": e(B * Lp, px.attn_hidden_size), "pr": e(B * Lp, px.attn_hidden_size),
+            "ex": e(B * Lp, pp * K.PIXEL_WIDTH),
+            "qp": e(B, px.num_heads, l_pad, HEAD_DIM), "kp": e(B, px.num_heads, l_pad, HEAD_DIM),
+            "vtp": torch.zeros(B, px.num_heads, HEAD_DIM, l_pad, device=dev, dtype=bf16),
+        }
+        # text-stream scratch of the dual blocks lives after the image rows of the shared buffers
+        key = ((hp, wp), T)
+        if key not in self._tables:
+            img = tables.rope_2d_angles(HEAD_DIM, hp, wp, cfg.rope_theta, cfg.rope_scale, cfg.rope_aspect,
+                                        cfg.rope_frame_pairs, cfg.rope_frame_theta)
+            pix = tables.rope_2d_angles(px.attn_hidden_size // px.num_heads, hp, wp, cfg.rope_theta,
+                                        cfg.rope_scale, cfg.rope_aspect)
+            txt = tables.rope_1d_angles(HEAD_DIM, T, cfg.text_rope_theta)
+            self._tables = {key: {
+                "rope": tables.cos_sin(txt, img, device=dev),
+                "rope_pix": tables.cos_sin(pix, device=dev),
+                "pos": tables.sincos_halves(K.PIXEL_WIDTH, shape.height, shape.width, dev),
+            }}
+        ws.update(self._tables[key])
+        self._ws, self._ws_shape = ws, shape
+        return ws
+
+    # -- forward ------------------------------------------------------------------------
+    @torch.no_grad()
+    def __call__(self, x: torch.Tensor, t: torch.Tensor, text: torch.Tensor, out: torch.Tensor | None = None):
+        """``x``: ``[B, 3, H, W]``; ``t``: model time ``[B]``; ``text``: ``[B, T, D]``; returns FP32 ``v``."""
+        cfg = self.cfg
+        p = cfg.patch_size
+        batch, channels, height, width = x.shape
+        if height % p or width % p:
+            raise ValueError(f"input {height}x{width} is not divisible by patch_size {p}")
+        if channels != cfg.in_channels:
+            raise ValueError(f"expected {cfg.in_channels} input channels, got {channels}")
+        if text.dim() != 3 or text.shape[0] != batch or text.shape[2] != cfg.hidden_size:
+            raise ValueError(f"text must be [B, T, {cfg.hidden_size}] prepared tokens, got {tuple(text.shape)}")
+        if t.numel() != batch:
+            raise ValueError(f"t must hold one model time per sample, got {tuple(t.shape)}")
+        dev = self.device
+        x = x.to(dev, torch.float32).contiguous()
+        t = t.reshape(batch).to(dev, torch.float32).contiguous()
+        text = text.to(dev, torch.float32).contiguous()
+        ws = self._workspace(_Shape(batch, height, width, text.shape[1]))
+        if out is None:
+            out = torch.empty(batch, 3, height, width, device=dev, dtype=torch.float32)
+        self._forward(ws, x, t, text, out)
+        return out
+
+    def _forward(self, ws: dict, x: torch.Tensor, t: torch.Tensor, text: torch.Tensor, out: torch.Tensor) -> None:
+        cfg, eps = self.cfg, self.eps
+        B = x.shape[0]
+        T, Lp, N = text.shape[1], ws["L"], ws["N"]
+        D = cfg.hidden_size
+        p = cfg.patch_size
+        pb0 = self.pixel_blocks[0]
+
+        # patch tokens, the pixel stream and its first norm, from one read of x
+        K.patchify_embed(x, p, self.pix_w, self.pix_b, ws["pos"][0], ws["pos"][1], pb0["norm1"], eps,
+                         ws["patches"], ws["pixels"], ws["hpix"])
+        K.linear(ws["patches"], self.s_w, self.s_b, out=ws["X"])
+
+        # timestep embedding, then both shared adaLN cores with every block's bias folded in
+        K.timestep_features(t, self.t_freqs, ws["tfeat"])
+        K.gemv(self.t0_w, ws["tfeat"], self.t0_b, ws["th"], out_silu=True)
+        K.gemv(self.t2_w, ws["th"], self.t2_b, ws["temb"])
+        K.gemv(self.core_img_w, ws["temb"], self.core_img_b, ws["mods_img"], extra_bias=self.img_bias, in_silu=True)
+        K.gemv(self.core_txt_w, ws["temb"], self.core_txt_b, ws["mods_txt"], extra_bias=self.txt_bias, in_silu=True)
+
+        Y = ws["Y"]
+        K.copy_rows(text.reshape(B * T, D), Y, B, T, 0, T, 0, T)
+        joined = False
+        for i, blk in enumerate(self.blocks):
+            if blk["kind"] == "mmdit":
+                self._dual_block(ws, blk, B, T, Lp, N)
+                continue
+            if not joined:
+                K.copy_rows(Y, ws["tok"], B, T, 0, T, 0, N)
+                K.copy_rows(ws["X"], ws["tok"], B, Lp, 0, Lp, T, N)
+                joined = True
+            self._single_block(ws, blk, B, T, Lp, N, last=i == cfg.depth - 1)
+
+        # pixel stage
+        K.silu_add_rows(ws["X"], ws["temb"], Lp, ws["scond"])
+        for j, pblk in enumerate(self.pixel_blocks):
+            next_norm = self.pixel_blocks[j + 1]["norm1"] if j + 1 < len(self.pixel_blocks) else self.final_norm
+            self._pixel_block(ws, pblk, B, Lp, next_norm)
+        K.unpatchify_head(ws["hpix"], self.final_w, self.final_b, out, p)
+
+    def _mods(self, ws: dict, table: str, index: int, chunk: int) -> torch.Tensor:
+        D = self.cfg.hidden_size
+        return ws[table][index][:, chunk * D:(chunk + 1) * D].unsqueeze(1)
+
+    def _dual_block(self, ws: dict, blk: dict, B: int, T: int, Lp: int, N: int) -> None:
+        cfg, eps = self.cfg, self.eps
+        D, H, Hkv = cfg.hidden_size, cfg.num_heads, cfg.kv_heads
+        X, Y = ws["X"], ws["Y"]
+        mi, mt = blk["img_mod"], blk["txt_mod"]
+        xm = [self._mods(ws, "mods_img", mi, c) for c in range(6)]
+        ym = [self._mods(ws, "mods_txt", mt, c) for c in range(6)]
+        qkvg_w = ws["qkvg"].shape[1]
+        rows_x, rows_y = B * Lp, B * T
+        hx, hy = ws["h_tok"][:rows_x], ws["h_tok"][rows_x:rows_x + rows_y]
+        px, py = ws["qkvg"][:rows_x], ws["qkvg"][rows_x:rows_x + rows_y]
+        ax, ay = ws["attn"][:rows_x], ws["attn"][rows_x:rows_x + rows_y]
+        bx, by = ws["branch"][:rows_x], ws["branch"][rows_x:rows_x + rows_y]
+        hhx, hhy = ws["hh"][:rows_x], ws["hh"][rows_x:rows_x + rows_y]
+
+        K.rms_norm_modulate(X.view(B, Lp, D), blk["norm_x1"], xm[0], xm[1], eps, torch.bfloat16, out=hx.view(B, Lp, D))
+        K.rms_norm_modulate(Y.view(B, T, D), blk["norm_y1"], ym[0], ym[1], eps, torch.bfloat16, out=hy.view(B, T, D))
+        K.linear_grouped([hx, hy], [blk["qkvg_x"], blk["qkvg_y"]], None, [px, py])
+        rope_c, rope_s = ws["rope"]
+        q, k, vt = ws["q"], ws["k"], ws["vt"]
+        for proj, st, rows, off in ((py, "y", T, 0), (px, "x", Lp, T)):
+            pv = proj.view(B, rows, qkvg_w)
+            K.qk_norm_rope(pv, blk[f"q_norm_{st}"], rope_c, rope_s, eps, H, 0, out=q, offset=off)
+            K.qk_norm_rope(pv, blk[f"k_norm_{st}"], rope_c, rope_s, eps, Hkv, H * HEAD_DIM, out=k, offset=off)
+            K.v_heads_t(pv, Hkv, vt, (H + Hkv) * HEAD_DIM, off)
+        gate_col = (H + 2 * Hkv) * HEAD_DIM
+        K.flash_attention(q, k, vt, N, ay, ax, n_split=T, gate0=py[:, gate_col:], gate1=px[:, gate_col:])
+        K.linear_grouped([ax, ay], [blk["proj_x_w"], blk["proj_y_w"]], [blk["proj_x_b"], blk["proj_y_b"]], [bx, by])
+        K.gated_residual_rms_norm_(X.view(B, Lp, D), bx.view(B, Lp, D), blk["attn_post_norm_x"], xm[2], eps)
+        K.gated_residual_rms_norm_(Y.view(B, T, D), by.view(B, T, D), blk["attn_post_norm_y"], ym[2], eps)
+        K.rms_norm_modulate(X.view(B, Lp, D), blk["norm_x2"], xm[3], xm[4], eps, torch.bfloat16, out=hx.view(B, Lp, D))
+        K.rms_norm_modulate(Y.view(B, T, D), blk["norm_y2"], ym[3], ym[4], eps, torch.bfloat16, out=hy.view(B, T, D))
+        K.linear_grouped([hx, hy], [blk["w13_x"], blk["w13_y"]], None, [hhx, hhy], swiglu=True)
+        K.linear_grouped([hhx, hhy], [blk["w2_x"], blk["w2_y"]], None, [bx, by])
+        K.gated_residual_rms_norm_(X.view(B, Lp, D), bx.view(B, Lp, D), blk["mlp_post_norm_x"], xm[5], eps)
+        K.gated_residual_rms_norm_(Y.view(B, T, D), by.view(B, T, D), blk["mlp_post_norm_y"], ym[5], eps)
+
+    def _single_block(self, ws: dict, blk: dict, B: int, T: int, Lp: int, N: int, last: bool) -> None:
+        cfg, eps = self.cfg, self.eps
+        D, H, Hkv = cfg.hidden_size, cfg.num_heads, cfg.kv_heads
+        tok = ws["tok"]
+        m = [self._mods(ws, "mods_img", blk["img_mod"], c) for c in range(6)]
+        rows = B * N
+        h, proj = ws["h_tok"][:rows], ws["qkvg"][:rows]
+        qkvg_w = proj.shape[1]
+        K.rms_norm_modulate(tok.view(B, N, D), blk["norm1"], m[0], m[1], eps, torch.bfloat16, out=h.view(B, N, D))
+        K.linear(h, blk["qkvg"], out=proj)
+        rope_c, rope_s = ws["rope"]
+        pv = proj.view(B, N, qkvg_w)
+        q, k, vt = ws["q"], ws["k"], ws["vt"]
+        K.qk_norm_rope(pv, blk["q_norm"], rope_c, rope_s, eps, H, 0, out=q, offset=0)
+        K.qk_norm_rope(pv, blk["k_norm"], rope_c, rope_s, eps, Hkv, H * HEAD_DIM, out=k, offset=0)
+        K.v_heads_t(pv, Hkv, vt, (H + Hkv) * HEAD_DIM, 0)
+        gate = proj[:, (H + 2 * Hkv) * HEAD_DIM:]
+        if not last:
+            R, M, per_batch = tok, rows, N
+            attn = ws["attn"][:rows]
+            K.flash_attention(q, k, vt, N, None, attn, n_split=0, gate1=gate)
+        else:
+            # the text rows still feed attention but no output depends on them (model.py:307-308)
+            R, M, per_batch = ws["X"], B * Lp, Lp
+            K.copy_rows(tok, R, B, Lp, T, N, 0, Lp)
+            attn = ws["attn"][:M]
+            K.flash_attention(q, k, vt, N, None, attn, n_split=T, gate1=gate[T:],
+                              out_batch_rows=(T, Lp), gate_batch_rows=(T, N))
+        branch, hh = ws["branch"][:M], ws["hh"][:M]
+        h2 = ws["h_tok"][:M]
+        K.linear(attn, blk["proj_w"], blk["proj_b"], out=branch)
+        K.gated_residual_rms_norm_(R.view(B, per_batch, D), branch.view(B, per_batch, D), blk["attn_post_norm"],
+                                   m[2], eps)
+        K.rms_norm_modulate(R.view(B, per_batch, D), blk["norm2"], m[3], m[4], eps, torch.bfloat16,
+                            out=h2.view(B, per_batch, D))
+        K.linear(h2, blk["w13"], out=hh, swiglu=True)
+        K.linear(hh, blk["w2"], out=branch)
+        K.gated_residual_rms_norm_(R.view(B, per_batch, D), branch.view(B, per_batch, D), blk["mlp_post_norm"],
+                                   m[5], eps)
+
+    def _pixel_block(self, ws: dict, blk: dict, B: int, Lp: int, next_norm: torch.Tensor) -> None:
+        cfg, eps = self.cfg, self.eps
+        px = cfg.pixel
+        heads = px.num_heads
+        width = px.attn_hidden_size
+        K.linear(ws["scond"], blk["adaln_w"], blk["adaln_b"], out=ws["mods_pix"].view(B * Lp, -1))
+        K.linear(ws["hpix"].view(B * Lp, -1), blk["compress_w"], blk["compress_b"], out=ws["cp"])
+        K.linear(ws["cp"], blk["qkv_w"], out=ws["pq"])
+        rope_c, rope_s = ws["rope_pix"]
+        pv = ws["pq"].view(B, Lp, 3 * width)
+        K.qk_norm_rope(pv, blk["q_norm"], rope_c, rope_s, eps, heads, 0, out=ws["qp"])
+        K.qk_norm_rope(pv, blk["k_norm"], rope_c, rope_s, eps, heads, width, out=ws["kp"])
+        K.v_heads_t(pv, heads, ws["vtp"], 2 * width, 0)
+        K.flash_attention(ws["qp"], ws["kp"], ws["vtp"], Lp, None, ws["pa"], n_split=0)
+        K.linear(ws["pa"], blk["proj_w"], blk["proj_b"], out=ws["pr"])
+        K.linear(ws["pr"], blk["expand_w"], blk["expand_b"], out=ws["ex"])
+        K.pixel_mlp_(ws["pixels"], ws["ex"].view_as(ws["hpix"]), ws["mods_pix"], blk["norm2"],
+                     (blk["fc1_w"], blk["fc1_b"]), (blk["fc2_w"], blk["fc2_b"]), next_norm, eps,
+                     next_input=ws["hpix"])
+
+    # -- conditioning -------------------------------------------------------------------
+    def encode_text(self, states: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """Encoder states ``[B, T, layers, dim]`` -> trunk text tokens (src/iris_metal/model.py:133-145).
+
+        The layer-attentive text adapter runs once per prompt and is not part of the denoise
+        step; it is not implemented on the GPU yet, so callers pass prepared tokens."""
+        raise NotImplementedError("HipIris.encode_text: the text adapter is not on the HIP path yet; "
+                                  "pass prepared text tokens [B, T, D] to __call__")

@@ -1,0 +1,91 @@
+"""Samplers around the velocity predictor, with their updates on the GPU.
+
+- ``turbo_sample``: the deterministic few-step flow-Euler loop of Iris-3B Turbo
+  (src/iris3b/sampling.py:98-138, sigmas of src/iris_metal/turbo.py:12). The update runs as
+  one FP32 kernel per step in the reference's operation order, the time values are staged
+  on the device before the loop, and the only host synchronisation is the finiteness check
+  of the final sample.
+- ``dpm1_sample``: first-order ``FlowDPMSolver`` (flow-Euler in log-SNR form) with
+  classifier-free guidance (src/iris3b/flow/solver.py:36-141, ``order=1``).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import kernels as K
+from .engine import require_finite
+
+TURBO_SIGMAS = (1.0, 0.938, 0.833, 0.625)
+
+
+@torch.no_grad()
+def turbo_sample(model, noise: torch.Tensor, text: torch.Tensor, sigmas=TURBO_SIGMAS,
+                 num_train_timesteps: int = 1000, check=require_finite) -> torch.Tensor:
+    """``model(x, t_model, text) -> v``; returns ``clean.clamp(-1, 1)`` after ``len(sigmas)`` steps."""
+    dev = text.device
+    x = noise.to(dev, torch.float32).contiguous()
+    batch = x.shape[0]
+    # t = float32(sigma) * num_train_timesteps in FP32, as the reference's sigma tensor
+    times = [torch.full((batch,), s, dtype=torch.float32) * num_train_timesteps for s in sigmas]
+    times = [t.to(dev) for t in times]
+    sig32 = [float(torch.tensor(s, dtype=torch.float32)) for s in sigmas]
+    clean = torch.empty_like(x)
+    x_next = torch.empty_like(x)
+    v = torch.empty_like(x)
+    for i in range(len(sigmas)):
+        model(x, times[i], text, out=v)
+        last = i + 1 == len(sigmas)
+        K.flow_euler(x, v, sig32[i], None if last else sig32[i + 1], None if last else x_next, clean)
+        if not last:
+            x, x_next = x_next, x
+    if check is not None:
+        check(clean)
+    out = torch.empty_like(clean)
+    K.clamp(clean, -1.0, 1.0, out)
+    return out
+
+
+def time_grid(steps: int, shift: float) -> list[float]:
+    """src/iris3b/flow/schedule.py:24-25 and solver.py:84-88."""
+    sigma = 1.0 - torch.linspace(1.0, 0.001, steps + 1, dtype=torch.float64)
+    return (shift * sigma / (1 + (shift - 1) * sigma)).flip(0).tolist()
+
+
+def _lam(t: float) -> float:
+    return math.inf if t <= 0.0 else math.log((1.0 - t) / t)
+
+
+@torch.no_grad()
+def dpm1_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor | None = None, steps: int = 20,
+                shift: float = 4.0, cfg_scale: float = 3.0, cfg_interval: tuple[float, float] = (0.0, 1.0),
+                num_timesteps: int = 1000) -> torch.Tensor:
+    """First-order ``FlowDPMSolver.sample`` with CFG batching ``cat([uncond, cond])``."""
+    grid = time_grid(steps, shift)
+    x = z.to(cond.device, torch.float32).contiguous()
+    batch = x.shape[0]
+    x2 = torch.empty((2 * batch, *x.shape[1:]), device=x.device, dtype=torch.float32)
+    text2 = torch.cat([uncond, cond]) if uncond is not None else None
+    v = torch.empty_like(x)
+    v2 = torch.empty_like(x2)
+    x_next = torch.empty_like(x)
+    flat = x.numel()
+    for i in range(1, steps + 1):
+        s, t = grid[i - 1], grid[i]
+        lo, hi = cfg_interval
+        use_cfg = uncond is not None and cfg_scale != 1.0 and lo < s < hi
+        rows = 2 * batch if use_cfg else batch
+        t_model = torch.full((rows,), s * num_timesteps, dtype=torch.float32, device=x.device)
+        if use_cfg:
+            for half in (0, 1):  # x2 = cat([x, x])
+                K.copy_rows(x.reshape(1, flat), x2.reshape(2, flat), 1, 1, 0, 1, half, 2)
+            model(x2, t_model, text2, out=v2)
+            K.cfg_combine(v2[:batch], v2[batch:], cfg_scale, v)
+        else:
+            model(x, t_model, cond, out=v)
+        phi1 = math.expm1(-(_lam(t) - _lam(s)))
+        K.dpm1_update(x, v, s, t / s, (1.0 - t) * phi1, x_next)
+        x, x_next = x_next, x
+    return x

@@ -1,0 +1,345 @@
+"""Each HIP kernel against the FP32 CPU oracle (or an FP32 PyTorch expression of the same op)
+on seeded inputs. Tolerances: FP32 outputs to FP32 rounding (summation order differs);
+BF16 outputs to one BF16 rounding of the FP32 result; MFMA products to the BF16 operand
+rounding they are specified with (FP32 accumulation)."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from iris_mi355x import _lib
+from iris_mi355x import kernels as K
+from oracle import iris_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def gen(seed=0):
+    return torch.Generator().manual_seed(seed)
+
+
+def close_bf16(got, want, scale=None, floor=1e-3):
+    """|got - want| within ~1.5 BF16 ulps of the magnitude (plus a floor)."""
+    got, want = got.float().cpu(), want.float().cpu()
+    tol = 6e-3 * want.abs() + floor * (scale if scale is not None else want.abs().max().item())
+    err = (got - want).abs()
+    assert torch.all(err <= tol), f"max err {err.max().item():.3e}, worst rel {(err / tol).max().item():.2f}x tol"
+
+
+# -- rows ------------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(1, 4352, 2560), (2, 37, 256), (3, 7, 384)])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_rms_norm_modulate(shape, x_dtype):
+    b, n, d = shape
+    g = gen(1)
+    x = torch.randn(shape, generator=g).to(x_dtype)
+    w = 1 + 0.02 * torch.randn(d, generator=g)
+    mods = 0.1 * torch.randn(b, 1, 6 * d, generator=g)
+    shift, scale = mods[..., :d], mods[..., d:2 * d]  # strided chunks of one modulation vector
+    want = O.modulate(O.rms_norm(x.float(), w, 1e-6), shift, scale)
+    got = K.rms_norm_modulate(x.to(DEV), w.to(DEV), mods.to(DEV)[..., :d], mods.to(DEV)[..., d:2 * d], 1e-6,
+                              torch.bfloat16)
+    close_bf16(got, want)
+    got32 = K.rms_norm_modulate(x.to(DEV), w.to(DEV), shift.to(DEV), scale.to(DEV), 1e-6, torch.float32)
+    torch.testing.assert_close(got32.cpu(), want, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize("branch_dtype", [torch.bfloat16, torch.float32])
+def test_gated_residual_rms_norm(branch_dtype):
+    b, n, d = 2, 300, 2560
+    g = gen(2)
+    res = torch.randn(b, n, d, generator=g)
+    branch = torch.randn(b, n, d, generator=g).to(branch_dtype)
+    w = 1 + 0.02 * torch.randn(d, generator=g)
+    gate = 0.1 * torch.randn(b, 1, d, generator=g)
+    want = res + gate * O.rms_norm(branch.float(), w, 1e-6)
+    r = res.to(DEV)
+    out = K.gated_residual_rms_norm_(r, branch.to(DEV), w.to(DEV), gate.to(DEV), 1e-6)
+    assert out.data_ptr() == r.data_ptr()
+    torch.testing.assert_close(r.cpu(), want, rtol=1e-5, atol=1e-5)
+
+
+def _qk_reference(x, weight, cos, sin, heads, col_offset, eps=1e-6):
+    b, n, _ = x.shape
+    h = x[..., col_offset:col_offset + heads * 128].reshape(b, n, heads, 128).float()
+    normed = O.rms_norm(h, weight, eps)
+    cis = torch.complex(cos, sin)
+    rotated, _ = O.apply_rope(normed, normed, cis)
+    return rotated.transpose(1, 2)
+
+
+@pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
+def test_qk_norm_rope_offsets_and_layout(src_dtype):
+    """A text and an image projection land in one [B, H, N, 128] buffer at their offsets; rows
+    outside the written range stay untouched (tests/test_metal_engine.py:159-176)."""
+    b, t, l, heads = 2, 16, 48, 3
+    width = heads * 128 + 256
+    g = gen(3)
+    yt = torch.randn(b, t, width, generator=g).to(src_dtype)
+    xi = torch.randn(b, l, width, generator=g).to(src_dtype)
+    w = 1 + 0.1 * torch.randn(128, generator=g)
+    cis = torch.cat([O.rope_1d(128, t), O.rope_2d(128, 6, 8, aspect="isotropic")])
+    cos, sin = cis.real.contiguous(), cis.imag.contiguous()
+    n_out = t + l + 8
+    out = torch.zeros(b, heads, n_out, 128, device=DEV, dtype=torch.bfloat16)
+    cos_d, sin_d = torch.cat([cos, torch.zeros(8, 64)]).to(DEV), torch.cat([sin, torch.zeros(8, 64)]).to(DEV)
+    K.qk_norm_rope(yt.to(DEV), w.to(DEV), cos_d, sin_d, 1e-6, heads, col_offset=128, out=out, offset=0)
+    K.qk_norm_rope(xi.to(DEV), w.to(DEV), cos_d, sin_d, 1e-6, heads, col_offset=128, out=out, offset=t)
+    got = out.float().cpu()
+    want_t = _qk_reference(yt, w, cos[:t], sin[:t], heads, 128)
+    want_i = _qk_reference(xi, w, cos[t:], sin[t:], heads, 128)
+    close_bf16(got[:, :, :t], want_t, scale=4.0)
+    close_bf16(got[:, :, t:t + l], want_i, scale=4.0)
+    assert torch.all(got[:, :, t + l:] == 0)
+
+
+def test_qk_norm_rope_rejects_uncovered_rows():
+    x = torch.randn(1, 10, 256, device=DEV)
+    w = torch.ones(128, device=DEV)
+    cos = torch.ones(8, 64, device=DEV)
+    with pytest.raises(ValueError, match="do not cover"):
+        K.qk_norm_rope(x, w, cos, cos, 1e-6, 2)
+
+
+def test_v_heads_t_transposes_exactly():
+    b, n, heads = 2, 77, 5
+    x = torch.randn(b, n, 6400, generator=gen(4)).to(torch.bfloat16).to(DEV)
+    out = torch.zeros(b, heads, 128, 128, device=DEV, dtype=torch.bfloat16)
+    K.v_heads_t(x, heads, out, col_offset=3200, offset=16)
+    v = x[..., 3200:3200 + heads * 128].reshape(b, n, heads, 128).permute(0, 2, 3, 1)
+    assert torch.equal(out[..., 16:16 + n], v)
+    assert torch.all(out[..., :16] == 0) and torch.all(out[..., 16 + n:] == 0)
+
+
+# -- GEMM --------------------------------------------------------------------------------
+def _gemm_ref(a, w, bias=None):
+    out = a.float().cpu() @ w.float().cpu().T
+    return out if bias is None else out + bias.cpu()
+
+
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2])
+@pytest.mark.parametrize("mnk", [(300, 320, 128), (4096, 1280, 256), (1, 64, 64), (513, 260, 192)])
+def test_gemm_matches_fp32_reference(tile, mnk):
+    m, n, k = mnk
+    g = gen(5)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (0.05 * torch.randn(n, k, generator=g)).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g)
+    _lib.call("iris_gemm_force_tile", tile)
+    try:
+        out32 = K.linear(a.to(DEV), w.to(DEV), bias.to(DEV), out_dtype=torch.float32)
+        out16 = K.linear(a.to(DEV), w.to(DEV), None)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    want = _gemm_ref(a, w, bias)
+    torch.testing.assert_close(out32.cpu(), want, rtol=1e-4, atol=1e-4)
+    close_bf16(out16, want - bias)
+
+
+@pytest.mark.parametrize("shape", [(4352, 6400, 2560), (4096, 16384, 2560)])
+def test_gemm_trunk_shapes(shape):
+    m, n, k = shape
+    g = torch.Generator(device=DEV).manual_seed(6)
+    a = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16)
+    out = K.linear(a, w, out_dtype=torch.float32)
+    rows = torch.arange(0, m, 97)
+    want = a[rows].float().cpu() @ w.float().cpu().T
+    torch.testing.assert_close(out[rows].cpu(), want, rtol=1e-4, atol=2e-4)
+
+
+def test_gemm_swiglu_epilogue_and_grouped_streams():
+    d, hidden = 256, 682
+    hp = 704
+    g = gen(7)
+    w1, w3 = 0.05 * torch.randn(hidden, d, generator=g), 0.05 * torch.randn(hidden, d, generator=g)
+    packed = K.pack_swiglu(w1, w3, hp).to(torch.bfloat16)
+    xs = [torch.randn(m, d, generator=g).to(torch.bfloat16) for m in (200, 33)]
+    outs = [torch.full((m, hp), 7.0, device=DEV, dtype=torch.bfloat16) for m in (200, 33)]
+    K.linear_grouped([x.to(DEV) for x in xs], [packed.to(DEV)] * 2, None, outs, swiglu=True)
+    for x, o in zip(xs, outs):
+        a = x.float() @ w1.to(torch.bfloat16).float().T
+        b = x.float() @ w3.to(torch.bfloat16).float().T
+        want = F.silu(a) * b
+        close_bf16(o[:, :hidden], want)
+        assert torch.all(o[:, hidden:].float() == 0)  # zero-padded hidden columns
+
+
+# -- attention -----------------------------------------------------------------------------
+def _attn_inputs(b, h, hkv, n, seed):
+    g = gen(seed)
+    n_pad = (n + 63) // 64 * 64
+    q = torch.randn(b, h, n, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(b, hkv, n, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(b, hkv, n, 128, generator=g).to(torch.bfloat16)
+    qd = torch.zeros(b, h, n_pad, 128, dtype=torch.bfloat16)
+    kd = torch.zeros(b, hkv, n_pad, 128, dtype=torch.bfloat16)
+    vt = torch.zeros(b, hkv, 128, n_pad, dtype=torch.bfloat16)
+    qd[:, :, :n], kd[:, :, :n], vt[..., :n] = q, k, v.transpose(-1, -2)
+    return q, k, v, qd.to(DEV), kd.to(DEV), vt.to(DEV)
+
+
+@pytest.mark.parametrize("b,h,hkv,n", [(1, 2, 1, 52), (2, 4, 1, 200), (1, 8, 2, 130), (1, 2, 2, 300)])
+def test_flash_attention_small(b, h, hkv, n):
+    q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 8)
+    want = O.attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(b, n, h * 128)
+    out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+    K.flash_attention(qd, kd, vt, n, None, out, n_split=0)
+    # probabilities enter the P.V MFMA as BF16: ~2^-9 relative per term on top of the output rounding
+    close_bf16(out.view(b, n, -1), want, scale=1.0, floor=4e-3)
+
+
+def test_flash_attention_trunk_shape_with_gate_and_split():
+    """20 query / 5 K/V heads over 256 text + 4096 image tokens, gate fused, rows split."""
+    b, h, hkv, t, l = 1, 20, 5, 256, 4096
+    n = t + l
+    q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 9)
+    gate = torch.randn(n, h * 128, generator=gen(10)).to(torch.bfloat16)
+    oy = torch.zeros(t, h * 128, device=DEV, dtype=torch.bfloat16)
+    ox = torch.zeros(l, h * 128, device=DEV, dtype=torch.bfloat16)
+    gd = gate.to(DEV)
+    K.flash_attention(qd, kd, vt, n, oy, ox, n_split=t, gate0=gd[:t], gate1=gd[t:])
+    heads = [0, 7, 19]
+    got = torch.cat([oy, ox]).float().cpu().view(n, h, 128)
+    sel = torch.arange(0, n, 5)
+    for hh in heads:
+        qh = q[:, hh:hh + 1, sel].float()
+        kk = k[:, hh // 4:hh // 4 + 1].float()
+        vv = v[:, hh // 4:hh // 4 + 1].float()
+        want = O.attention(qh, kk, vv)[0, 0] * torch.sigmoid(gate[sel, hh * 128:(hh + 1) * 128].float())
+        close_bf16(got[sel, hh], want, scale=1.0, floor=4e-3)
+
+
+# -- conditioning, pixel stage, sampler ----------------------------------------------------
+def test_gemv_with_core_biases():
+    n, k, j, b = 1536, 256, 3, 2
+    g = gen(11)
+    w = (0.05 * torch.randn(n, k, generator=g)).to(torch.bfloat16)
+    x = torch.randn(b, k, generator=g)
+    bias, extra = torch.randn(n, generator=g), torch.randn(j, n, generator=g)
+    out = torch.empty(j, b, n, device=DEV)
+    K.gemv(w.to(DEV), x.to(DEV), bias.to(DEV), out, extra_bias=extra.to(DEV), in_silu=True)
+    y = F.silu(x) @ w.float().T + bias
+    torch.testing.assert_close(out.cpu(), y[None] + extra[:, None], rtol=1e-5, atol=1e-5)
+    out2 = torch.empty(b, n, device=DEV)
+    K.gemv(w.to(DEV), x.to(DEV), bias.to(DEV), out2, out_silu=True)
+    torch.testing.assert_close(out2.cpu(), F.silu(x @ w.float().T + bias), rtol=1e-5, atol=1e-5)
+
+
+def test_timestep_features():
+    from iris_mi355x import tables
+
+    t = torch.tensor([0.0, 125.0, 625.0, 1000.0])
+    freqs = tables.timestep_freqs(256, 10.0, "cpu")
+    out = torch.empty(4, 256, device=DEV)
+    K.timestep_features(t.to(DEV), freqs.to(DEV), out)
+    torch.testing.assert_close(out.cpu(), O.timestep_features(t, 256, 10.0), rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("hw,patch", [((32, 48), 4), ((64, 64), 16)])
+def test_patchify_embed_and_head(hw, patch):
+    from iris_mi355x import tables
+
+    b = 2
+    h, w = hw
+    g = gen(12)
+    x = torch.randn(b, 3, h, w, generator=g)
+    p = {"pixel_embedder.proj.weight": 0.5 * torch.randn(16, 3, generator=g),
+         "pixel_embedder.proj.bias": 0.1 * torch.randn(16, generator=g)}
+    nw = 1 + 0.02 * torch.randn(16, generator=g)
+    n_patches = (h // patch) * (w // patch)
+    kp = (3 * patch * patch + 63) // 64 * 64
+    patches = torch.zeros(b * n_patches, kp, device=DEV, dtype=torch.bfloat16)
+    pixels = torch.empty(b * n_patches, patch * patch, 16, device=DEV)
+    normed = torch.empty_like(pixels, dtype=torch.bfloat16)
+    pos_x, pos_y = tables.sincos_halves(16, h, w, DEV)
+    K.patchify_embed(x.to(DEV), patch, p["pixel_embedder.proj.weight"].to(DEV), p["pixel_embedder.proj.bias"].to(DEV),
+                     pos_x, pos_y, nw.to(DEV), 1e-6, patches, pixels, normed)
+    want_patches = O.patchify(x, patch).reshape(b * n_patches, -1)
+    assert torch.equal(patches[:, :3 * patch * patch].cpu(), want_patches.to(torch.bfloat16))
+    assert torch.all(patches[:, 3 * patch * patch:] == 0)
+    want_pix = O.pixel_embed(p, x, patch, True)
+    torch.testing.assert_close(pixels.cpu(), want_pix, rtol=1e-5, atol=1e-5)
+    close_bf16(normed, O.rms_norm(want_pix, nw, 1e-6))
+
+    hw_ = 0.3 * torch.randn(3, 16, generator=g)
+    hb = 0.1 * torch.randn(3, generator=g)
+    out = torch.empty(b, 3, h, w, device=DEV)
+    K.unpatchify_head(normed, hw_.to(DEV), hb.to(DEV), out, patch)
+    want = O.unpatchify(normed.float().cpu() @ hw_.T + hb, b, h, w, patch)
+    torch.testing.assert_close(out.cpu(), want, rtol=1e-5, atol=1e-5)
+
+
+def test_pixel_mlp_matches_post_modulated_tail():
+    n = 4096 * 3 + 17
+    g = gen(13)
+    pixels = torch.randn(n, 16, generator=g)
+    branch = torch.randn(n, 16, generator=g).to(torch.bfloat16)
+    mods = (0.3 * torch.randn(n, 64, generator=g)).to(torch.bfloat16)
+    nw, nnw = 1 + 0.1 * torch.randn(16, generator=g), 1 + 0.1 * torch.randn(16, generator=g)
+    fc1 = (0.3 * torch.randn(64, 16, generator=g), 0.1 * torch.randn(64, generator=g))
+    fc2 = (0.3 * torch.randn(16, 64, generator=g), 0.1 * torch.randn(16, generator=g))
+    p = {"m.fc1.weight": fc1[0], "m.fc1.bias": fc1[1], "m.fc2.weight": fc2[0], "m.fc2.bias": fc2[1]}
+    m = mods.float()
+    scale1, shift1, scale2, shift2 = m.chunk(4, dim=-1)
+    x = pixels + O.modulate(branch.float(), shift1, scale1)
+    x = x + O.modulate(O.gelu_mlp(p, "m", O.rms_norm(x, nw, 1e-6)), shift2, scale2)
+    want_next = O.rms_norm(x, nnw, 1e-6)
+    pd = pixels.to(DEV)
+    nxt = K.pixel_mlp_(pd, branch.to(DEV), mods.to(DEV), nw.to(DEV), fc1, fc2, nnw.to(DEV), 1e-6)
+    torch.testing.assert_close(pd.cpu(), x, rtol=2e-5, atol=2e-5)
+    close_bf16(nxt, want_next)
+
+
+def test_pixel_mlp_gelu_is_exact_erf():
+    """The exact-erf GELU of the pixel MLP against torch's, over 4096 BF16 arguments in
+    [-8, 8] (a zero norm gain makes every hidden pre-activation equal its bias, and an identity
+    fc2 routes hidden units 0..15 to the 16 output channels of a zero pixel stream)."""
+    args = torch.linspace(-8, 8, 4096).to(torch.bfloat16).float()
+    zeros16 = torch.zeros(16, device=DEV)
+    fc2 = (torch.eye(16, 64), torch.zeros(16))
+    got = []
+    for chunk in args.split(16):
+        pixels = torch.zeros(64, 16, device=DEV)
+        fc1_b = torch.zeros(64)
+        fc1_b[:16] = chunk
+        K.pixel_mlp_(pixels, torch.zeros(64, 16, device=DEV, dtype=torch.bfloat16),
+                     torch.zeros(64, 64, device=DEV, dtype=torch.bfloat16), zeros16,
+                     (torch.zeros(64, 16), fc1_b), fc2, torch.ones(16, device=DEV), 1e-6)
+        got.append(pixels[0].cpu())
+    got = torch.cat(got).double()
+    want = F.gelu(args.double())  # float64: the FP32 textbook formula itself cancels for a << 0
+    torch.testing.assert_close(got, want, rtol=4e-6, atol=1e-30)
+    torch.testing.assert_close(got.float(), F.gelu(args), rtol=2e-6, atol=1e-6)
+
+
+def test_flow_euler_is_bitwise_the_reference_update():
+    g = gen(14)
+    x, v = torch.randn(3, 64, 64, generator=g), torch.randn(3, 64, 64, generator=g)
+    for s, s_next in ((1.0, 0.938), (0.938, 0.833), (0.833, 0.625)):
+        sigma = torch.full((1,), s, dtype=torch.float32)
+        clean = x - sigma * v
+        implied = (x - (1 - sigma) * clean) / sigma
+        sn = torch.full((1,), s_next, dtype=torch.float32)
+        want = (1 - sn) * clean + sn * implied
+        xn, cl = torch.empty(3, 64, 64, device=DEV), torch.empty(3, 64, 64, device=DEV)
+        K.flow_euler(x.to(DEV), v.to(DEV), float(sigma), float(sn), xn, cl)
+        assert torch.equal(cl.cpu(), clean)
+        assert torch.equal(xn.cpu(), want)
+
+
+def test_cfg_combine_and_clamp():
+    g = gen(15)
+    u, c = torch.randn(1000, generator=g), torch.randn(1000, generator=g)
+    out = torch.empty(1000, device=DEV)
+    K.cfg_combine(u.to(DEV), c.to(DEV), 3.0, out)
+    assert torch.equal(out.cpu(), u + 3.0 * (c - u))
+    K.clamp(out, -1.0, 1.0, out)
+    assert torch.equal(out.cpu(), (u + 3.0 * (c - u)).clamp(-1, 1))
+
+
+def test_cpu_tensors_are_rejected():
+    with pytest.raises(ValueError, match="GPU"):
+        K.rms_norm_modulate(torch.randn(1, 2, 128), torch.ones(128), torch.zeros(1, 1, 128),
+                            torch.zeros(1, 1, 128), 1e-6, torch.bfloat16)
