@@ -1,24 +1,24 @@
 // BF16 GEMM on gfx950 MFMA: C[m, n] = sum_k A[m, k] * B[n, k] (+ bias[n]), FP32 accumulate.
 //
 // Both operands are K-contiguous ("NT"), the natural layout of nn.Linear weights, so every
-// MFMA operand fragment is one 16-byte LDS read. A 256-thread workgroup computes a BM x BN
-// tile with four waves in a 2 x 2 arrangement; each wave owns a (BM/2) x (BN/2) block built
-// from v_mfma_f32_32x32x16_bf16. The weight fragment is the MFMA's A operand and the
-// activation fragment its B operand, so each lane ends up holding four consecutive output
-// columns of one row: the epilogue stores 8 (BF16) or 16 (FP32) contiguous bytes per lane.
+// MFMA operand fragment is one 16-byte LDS read. A workgroup computes a BM x BN tile with
+// WGM x WGN waves; each wave owns a (BM/WGM) x (BN/WGN) block of v_mfma_f32_32x32x16_bf16
+// results. The weight fragment is the MFMA's A operand and the activation fragment its B
+// operand, so each lane ends up holding four consecutive output columns of one row: the
+// epilogue stores 8 (BF16) or 16 (FP32) contiguous bytes per lane.
 //
-// Pipeline: the K loop is double-buffered in LDS (rows padded to 144 bytes so the 16-lane
-// phases of ds_read_b128 hit 64 distinct banks); the next K tile is fetched into registers
-// while the current one feeds the MFMAs, then written to the other buffer; one barrier per
-// K tile. Workgroup ids are remapped so consecutive tiles (which share the weight tile)
-// run on the same XCD and hit its L2.
+// Data path: K tiles go global -> LDS with global_load_lds_dwordx4 (no register staging)
+// into a ring of STAGES buffers, XOR-swizzled so the MFMA fragment reads are bank-conflict
+// free. The fragments of the next k-step are read while the current MFMAs run, and the
+// wait + barrier for the next K tile is placed before the last k-step of the current one.
+// Workgroup ids are remapped so that the tiles running concurrently on one XCD form an
+// 8 x 4 block and share their operands through that XCD's L2.
 #include "iris_common.hpp"
 
 namespace iris {
 namespace {
 
 constexpr int kBK = 64;
-constexpr int kLdsStride = kBK + 8;  // elements per LDS row: 144 bytes
 
 struct GemmGroup {
   const bf16* a;
@@ -43,14 +43,46 @@ __device__ __forceinline__ void store_out4(TC* p, float v0, float v1, float v2, 
   store4(p, f32x4{v0, v1, v2, v3});
 }
 
-template <int BM, int BN, int EPI, typename TC>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Same, and also all LDS reads of this wave (lgkmcnt = 0).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+// LDS layout: each operand tile is BM (or BN) rows of BK bf16, unpadded; the 16-byte chunk c
+// of row r is stored at chunk c ^ swz(r) so that the 16 rows read by one ds_read_b128 phase
+// cover all 64 banks. Tiles are filled by global_load_lds_dwordx4, which writes lane i's
+// 16 bytes at LDS base + 16 i: each lane therefore fetches the global chunk that belongs
+// at its LDS position.
+template <int BK>
+__device__ __forceinline__ int swz(int r) {
+  constexpr int CPR = BK / 8;
+  return (r / (16 / CPR)) % CPR;
+}
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int EPI, typename TC>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
+  constexpr int NW = WGM * WGN;             // waves per workgroup
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int FM = WM / 32, FN = WN / 32;
-  constexpr int A_CHUNKS = BM * kBK / 8 / 256;
-  constexpr int B_CHUNKS = BN * kBK / 8 / 256;
-  constexpr int STAGE = (BM + BN) * kLdsStride;
-  __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE];
+  constexpr int KS = BK / 16;               // MFMA k-steps per K tile
+  constexpr int CPR = BK / 8;               // 16-byte chunks per row
+  constexpr int RPL = 64 / CPR;             // rows per wave-wide 1 KB load
+  constexpr int A_LOADS = BM / RPL / NW;    // load instructions per wave per stage
+  constexpr int B_LOADS = BN / RPL / NW;
+  constexpr int LPW = A_LOADS + B_LOADS;
+  constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
+  static_assert(A_LOADS * RPL * NW == BM && B_LOADS * RPL * NW == BN, "tile / wave split");
+  static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
   int tile = xcd_remap(blockIdx.x, p.total_tiles);
   const bool second = p.ngroups > 1 && tile >= p.g1.tile_begin;
@@ -61,78 +93,112 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
   const int M = second ? p.g1.m : p.g0.m;
   const int tiles_m = second ? p.g1.tiles_m : p.g0.tiles_m;
   tile -= second ? p.g1.tile_begin : 0;
-  const int tn = tile / tiles_m;
-  const int tm = tile - tn * tiles_m;
   const int N = p.n;
-  const long lda = p.lda, ldb = p.ldb;
+  const int tiles_n = (N + BN - 1) / BN;
+  // groups of 8 row tiles sweep all column tiles: ~32 concurrent tiles of one XCD form an
+  // 8 x 4 block, so both operands are re-read from that XCD's L2
+  constexpr int GM = 8;
+  const int group = tile / (GM * tiles_n);
+  const int gm = min(GM, tiles_m - group * GM);
+  const int in_group = tile - group * GM * tiles_n;
+  const int tm = group * GM + in_group % gm;
+  const int tn = in_group / gm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int g = lane >> 5;
   const int w = tid >> 6;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / WGN, wn = w % WGN;
 
-  // global -> register fetch addresses: chunk idx = tid + 256 i -> row idx / 8, column chunk idx % 8
-  const int ld_row = tid >> 3;
-  const int ld_col = (tid & 7) * 8;
-  // 32-bit element offsets (the host checks m * lda and n * ldb stay below 2^31)
-  int a_off[A_CHUNKS], b_off[B_CHUNKS];
+  // per-lane global offsets of the chunks this lane fetches (32-bit; host checks the range)
+  const int ld_r = lane / CPR;
+  const int ld_p = lane % CPR;
+  int a_off[A_LOADS], b_off[B_LOADS];
 #pragma unroll
-  for (int i = 0; i < A_CHUNKS; ++i)
-    a_off[i] = min(tm * BM + ld_row + 32 * i, M - 1) * static_cast<int>(lda) + ld_col;
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int r = (w * A_LOADS + i) * RPL + ld_r;
+    a_off[i] = min(tm * BM + r, M - 1) * static_cast<int>(p.lda) + 8 * (ld_p ^ swz<BK>(r));
+  }
 #pragma unroll
-  for (int i = 0; i < B_CHUNKS; ++i)
-    b_off[i] = min(tn * BN + ld_row + 32 * i, N - 1) * static_cast<int>(ldb) + ld_col;
+  for (int i = 0; i < B_LOADS; ++i) {
+    const int r = (w * B_LOADS + i) * RPL + ld_r;
+    b_off[i] = min(tn * BN + r, N - 1) * static_cast<int>(p.ldb) + 8 * (ld_p ^ swz<BK>(r));
+  }
+  auto issue = [&](int kt, int stage) {
+    bf16* sa = lds + stage * STAGE;
+    bf16* sb = sa + A_STAGE;
+    // (explicit void* casts: without them the host pass silently drops the kernel stub)
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(A + a_off[i] + kt * BK),
+                                       (void*)(sa + (w * A_LOADS + i) * RPL * BK), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(B + b_off[i] + kt * BK),
+                                       (void*)(sb + (w * B_LOADS + i) * RPL * BK), 16, 0, 0);
+  };
 
-  bf16x8 ra[A_CHUNKS], rb[B_CHUNKS];
+  // fragment reads: row r, logical chunk 2 ks + g, stored at chunk (2 ks + g) ^ swz(r)
+  int a_row[FM], b_row[FN];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) a_row[j] = wm * WM + j * 32 + l32;
+#pragma unroll
+  for (int i = 0; i < FN; ++i) b_row[i] = wn * WN + i * 32 + l32;
+  bf16x8 wf[2][FN], xf[2][FM];
+  auto read_frags = [&](int stage, int ks, int buf) {
+    const bf16* sa = lds + stage * STAGE;
+    const bf16* sb = sa + A_STAGE;
+    const int c = 2 * ks + g;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+      wf[buf][i] = *reinterpret_cast<const bf16x8*>(sb + b_row[i] * BK + 8 * (c ^ swz<BK>(b_row[i])));
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+      xf[buf][j] = *reinterpret_cast<const bf16x8*>(sa + a_row[j] * BK + 8 * (c ^ swz<BK>(a_row[j])));
+  };
+
   f32x16 acc[FN][FM];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
 
-  const int KT = p.k / kBK;
-  auto fetch = [&](int kt) {
+  // Software pipeline: the fragments of the next k-step are read from LDS while the MFMAs
+  // of the current one run; the wait + barrier for K tile kt+1 sits before the last k-step
+  // of tile kt, whose fragments are already in registers, so the stage being retired can be
+  // refilled right after that barrier.
+  const int KT = p.k / BK;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) ra[i] = *reinterpret_cast<const bf16x8*>(A + a_off[i] + kt * kBK);
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i) rb[i] = *reinterpret_cast<const bf16x8*>(B + b_off[i] + kt * kBK);
-  };
-  auto stash = [&](int buf) {
-    bf16* As = lds + buf * STAGE;
-    bf16* Bs = As + BM * kLdsStride;
-#pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i)
-      *reinterpret_cast<bf16x8*>(As + (ld_row + 32 * i) * kLdsStride + ld_col) = ra[i];
-#pragma unroll
-    for (int i = 0; i < B_CHUNKS; ++i)
-      *reinterpret_cast<bf16x8*>(Bs + (ld_row + 32 * i) * kLdsStride + ld_col) = rb[i];
-  };
-
-  fetch(0);
-  stash(0);
-  __syncthreads();
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KT) issue(s, s);
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  if (STAGES - 1 < KT) issue(STAGES - 1, STAGES - 1);
+  read_frags(0, 0, 0);
   for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) fetch(kt + 1);
-    const bf16* As = lds + cur * STAGE + (wm * WM + l32) * kLdsStride + g * 8;
-    const bf16* Bs = lds + cur * STAGE + BM * kLdsStride + (wn * WN + l32) * kLdsStride + g * 8;
+    const int stage = kt % STAGES;
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      bf16x8 wf[FN], xf[FM];
-#pragma unroll
-      for (int i = 0; i < FN; ++i) wf[i] = *reinterpret_cast<const bf16x8*>(Bs + i * 32 * kLdsStride + ks * 16);
-#pragma unroll
-      for (int j = 0; j < FM; ++j) xf[j] = *reinterpret_cast<const bf16x8*>(As + j * 32 * kLdsStride + ks * 16);
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KS) {
+        read_frags(stage, ks + 1, cur ^ 1);
+      } else if (kt + 1 < KT) {
+        // this wave's fragment reads of stage kt must have landed before the stage is refilled
+        if (kt + STAGES - 1 < KT)
+          wait_vmcnt_lgkm0<(STAGES - 2) * LPW>();
+        else
+          wait_vmcnt_lgkm0<0>();
+        __builtin_amdgcn_s_barrier();
+        if (kt + STAGES < KT) issue(kt + STAGES, stage);
+        read_frags((kt + 1) % STAGES, 0, cur ^ 1);
+      }
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], xf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cur][i], xf[cur][j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < KT) stash(cur ^ 1);
-    __syncthreads();
   }
 
   // epilogue: acc[i][j][r] = C[m, n] with n = tile + 8 (r / 4) + 4 g + r % 4, m = tile + l32
@@ -177,32 +243,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
 int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   const dim3 grid(args.total_tiles);
+  const dim3 block(64 * WGM * WGN);
   if (epilogue == IRIS_EPI_SILU_MUL) {
     if (c_dtype == IRIS_BF16)
-      gemm_kernel<BM, BN, IRIS_EPI_SILU_MUL, bf16><<<grid, 256, 0, stream>>>(args);
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, bf16><<<grid, block, 0, stream>>>(args);
     else
-      gemm_kernel<BM, BN, IRIS_EPI_SILU_MUL, float><<<grid, 256, 0, stream>>>(args);
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, float><<<grid, block, 0, stream>>>(args);
   } else {
     if (c_dtype == IRIS_BF16)
-      gemm_kernel<BM, BN, IRIS_EPI_NONE, bf16><<<grid, 256, 0, stream>>>(args);
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_NONE, bf16><<<grid, block, 0, stream>>>(args);
     else
-      gemm_kernel<BM, BN, IRIS_EPI_NONE, float><<<grid, 256, 0, stream>>>(args);
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_NONE, float><<<grid, block, 0, stream>>>(args);
   }
   return check_launch("gemm_bf16");
 }
 
-// Tile shape: the largest tile that still gives about one full round of workgroups on the
-// 256 CUs; smaller tiles trade MFMA intensity for occupancy on the N = 1280 / 2560 shapes.
+struct TileShape {
+  int bm, bn, bk, stages;
+};
+// 0: 256x256 BK64 x2 (4 waves), 1: 256x256 BK32 x4 (4 waves), 2: 256x256 BK64 x2 (8 waves),
+// 3: 128x128 BK64 x2 (4 waves, 2 workgroups per CU), 4: 256x256 BK32 x4 (8 waves),
+// 5: 256x128 BK64 x2 (4 waves)
+constexpr TileShape kTiles[] = {{256, 256, 64, 2}, {256, 256, 32, 4}, {256, 256, 64, 2},
+                                {128, 128, 64, 2}, {256, 256, 32, 4}, {256, 128, 64, 2}};
+constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+
+// Tile shape (measured on the trunk and pixel-stage shapes): 256x256 with 8 waves once there
+// are enough tiles to cover the 256 CUs, else 128x128 (two workgroups per CU).
 int pick_tile(long m_total, int n, int forced) {
   if (forced >= 0) return forced;
   const long t256 = ((m_total + 255) / 256) * ((n + 255) / 256);
-  if (t256 >= 224) return 0;
-  const long t256x128 = ((m_total + 255) / 256) * ((n + 127) / 128);
-  if (t256x128 >= 224) return 1;
-  return 2;
+  return t256 >= 160 ? 2 : 3;
 }
 
 int g_forced_tile = -1;
@@ -243,8 +317,9 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   for (int i = 0; i < groups; ++i)
     IRIS_REQUIRE(static_cast<long>(m[i]) * lda < (1L << 31), "gemm: activation too large for 32-bit offsets");
   const int tile = pick_tile(m_total, n, g_forced_tile);
-  const int bm = tile == 2 ? 128 : 256;
-  const int bn = tile == 0 ? 256 : 128;
+  const TileShape shape = kTiles[tile];
+  const int bm = shape.bm;
+  const int bn = shape.bn;
   const int tiles_n = (n + bn - 1) / bn;
   int begin = 0;
   GemmGroup* gs[2] = {&args.g0, &args.g1};
@@ -264,11 +339,17 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   if (begin == 0) return IRIS_OK;
   switch (tile) {
     case 0:
-      return launch_tile<256, 256>(args, c_dtype, epilogue, stream);
+      return launch_tile<256, 256, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
     case 1:
-      return launch_tile<256, 128>(args, c_dtype, epilogue, stream);
+      return launch_tile<256, 256, 32, 4, 2, 2>(args, c_dtype, epilogue, stream);
+    case 2:
+      return launch_tile<256, 256, 64, 2, 2, 4>(args, c_dtype, epilogue, stream);
+    case 3:
+      return launch_tile<128, 128, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
+    case 4:
+      return launch_tile<256, 256, 32, 4, 2, 4>(args, c_dtype, epilogue, stream);
     default:
-      return launch_tile<128, 128>(args, c_dtype, epilogue, stream);
+      return launch_tile<256, 128, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
   }
 }
 
@@ -282,9 +363,9 @@ extern "C" int iris_gemm_bf16(const void* a, const void* b, const float* bias, v
   return iris_gemm_bf16_grouped(1, as, bs, biases, cs, ms, c_dtype, n, k, lda, ldb, ldc, epilogue, stream);
 }
 
-// Tuning hook: force a tile shape (0: 256x256, 1: 256x128, 2: 128x128, -1: automatic).
+// Tuning hook: force a tile shape (an index into kTiles, -1: automatic).
 extern "C" int iris_gemm_force_tile(int tile) {
-  IRIS_REQUIRE(tile >= -1 && tile <= 2, "gemm_force_tile: tile in -1..2");
+  IRIS_REQUIRE(tile >= -1 && tile < kNumTiles, "gemm_force_tile: tile in -1..%d", kNumTiles - 1);
   g_forced_tile = tile;
   return IRIS_OK;
 }
