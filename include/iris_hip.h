@@ -59,15 +59,19 @@ int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int dst_dtype, 
                       hipStream_t stream);
 
 /* The V half of the attention input (src/iris_metal/model.py:243-250 builds [B,Hkv,N,128]):
- * heads at col_offset of a BF16 [batch, n_src, row_stride] projection are written transposed,
- * dst[b, h, d, dst_offset + token] in a BF16 [batch, heads, 128, n_dst] buffer. */
+ * heads at col_offset of a BF16 [batch, n_src, row_stride] projection are written transposed
+ * into a BF16 [batch, heads, 128, n_dst] buffer (n_dst % 64 == 0): token dst_offset + t goes to
+ * position s(dst_offset + t), where s swaps the 4-position quads 1 and 2 of every group of 16
+ * (positions 4..7 <-> 8..11), the layout iris_flash_attn reads. Other positions are untouched. */
 int iris_v_heads_t(const void* src, void* dst, int batch, long n_src, long n_dst, int heads, long dst_offset,
                    long row_stride, long col_offset, hipStream_t stream);
 
 /* softmax(q k^T * scale) v over a joint sequence of n tokens (F.scaled_dot_product_attention
  * with GQA, src/iris_metal/model.py:243-250; src/iris3b/nn/attention.py:61-91).
  * q: BF16 [batch, heads, n_pad, 128]; k: BF16 [batch, kv_heads, n_pad, 128];
- * vt: BF16 [batch, kv_heads, 128, n_pad] with zeros in columns >= n; n_pad = n rounded up to 64.
+ * vt: BF16 [batch, kv_heads, 128, n_pad] as written by iris_v_heads_t (V transposed, the two middle
+ * 4-token quads of every 16 positions swapped), zero at the positions of tokens >= n;
+ * n_pad = n rounded up to 64.
  * Output row r of batch b goes to out0 row (b*out_batch_rows0 + r) when r < n_split, else to out1
  * row (b*out_batch_rows1 + r - n_split), column h*128 + d, BF16, row stride ld_out; a null out
  * pointer skips its rows. With gate0/gate1 (rows b*gate_batch_rows{0,1} + r or r - n_split,
@@ -77,6 +81,11 @@ int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int
                     long n_pad, long n_split, float scale, void* out0, void* out1, long ld_out,
                     long out_batch_rows0, long out_batch_rows1, const void* gate0, const void* gate1, long ld_gate,
                     long gate_batch_rows0, long gate_batch_rows1, hipStream_t stream);
+
+/* Tuning hook for the benchmark sweep: force the attention variant (0: 64 query rows per wave,
+ * 2 K/V stages; 1: 64 rows, 3 stages; 2: 32 rows, 2 stages) or restore the automatic choice (-1).
+ * No counterpart in the reference. */
+int iris_flash_attn_force_variant(int variant);
 
 /* F.linear on bf16 MFMA (src/iris_metal/model.py:46-52): C[m, n] = sum_k A[m, k] B[n, k] + bias[n]
  * with A BF16 [m, lda], B (the weight) BF16 [n, ldb], C in c_dtype with row stride ldc.

@@ -32,6 +32,7 @@ _SIGNATURES: dict[str, list] = {
                         c_long, P, P, c_long, c_long, c_long, P],
     "iris_gemm_bf16": [P, P, P, P, c_int, c_int, c_int, c_int, c_long, c_long, c_long, c_int, P],
     "iris_gemm_force_tile": [c_int],
+    "iris_flash_attn_force_variant": [c_int],
     "iris_gemm_bf16_grouped": [c_int, P, P, P, P, P, c_int, c_int, c_int, c_long, c_long, c_long, c_int, P],
     "iris_gemv_bf16": [P, P, c_int, c_int, c_int, P, P, c_int, P, c_int, c_int, P],
     "iris_timestep_features": [P, P, c_int, c_int, P, P],

@@ -2,28 +2,31 @@
 // K/V heads and the attention gate fused into the store.
 //
 // Workgroup = 4 waves sharing one K/V head: with G = heads / kv_heads query heads per K/V
-// head, a workgroup serves hpw = min(G, 4) of them and 64 * 4 / hpw query rows, one wave per
-// (query head, 64-row block). K/V tiles of 64 keys are staged through LDS once and read by
-// all four waves, double-buffered with a register prefetch.
+// head, a workgroup serves hpw = min(G, 4) of them and 32 * QB * 4 / hpw query rows, one
+// wave per (query head, 32*QB-row block). K/V tiles of 64 keys go global -> LDS with
+// global_load_lds_dwordx4 (no register staging) into a ring of STAGES buffers, and are
+// read by all four waves.
 //
 // Each wave computes S^T = K Q^T (v_mfma_f32_32x32x16_bf16, K fragments from LDS, Q
 // fragments held in registers), so every lane owns one query column and 32 of the 64 keys
 // of the tile: the online-softmax row max / sum need a single cross-lane exchange (lane ^ 32).
 // The probabilities, converted to bf16 in place, are exactly the B operand of O^T = V^T P^T
 // (with a fixed permutation of the keys inside each 16-key step, applied identically to the
-// V^T fragments), so P never leaves registers. V arrives pre-transposed ([d, token]) so that
-// V^T fragments are plain LDS reads.
+// V^T fragments), so P never leaves registers. V arrives transposed ([d, token]) with the
+// middle two 4-key quads of every 16 keys swapped, so each V^T fragment is one 16-byte read.
+//
+// LDS: K rows are 256 bytes, chunk c of key row r at chunk c ^ (r % 16); V^T rows are 128
+// bytes, chunk c of row d at c ^ ((d / 2) % 8): the 16-lane phases of ds_read_b128 hit
+// 64 distinct banks.
 #include "iris_common.hpp"
 
 namespace iris {
 namespace {
 
 constexpr int kHd = 128;
-constexpr int kKv = 64;               // keys per tile
-constexpr int kKStride = kHd + 8;     // LDS row of K: 272 bytes (16 lanes -> 64 distinct banks)
-constexpr int kVStride = kKv + 4;     // LDS row of V^T: 136 bytes (32 lanes -> 64 distinct banks)
-constexpr int kKTile = kKv * kKStride;
-constexpr int kVTile = kHd * kVStride;
+constexpr int kKv = 64;                  // keys per tile
+constexpr int kTile = kKv * kHd;         // elements of one K (or V^T) tile
+constexpr int kLoadsPerWave = 4;         // 1 KB loads per wave per operand per tile
 
 struct AttnArgs {
   const bf16* q;
@@ -41,9 +44,18 @@ struct AttnArgs {
   float scale_log2;
 };
 
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int QB, int STAGES>
 __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) bf16 k_lds[2 * kKTile];
-  __shared__ __attribute__((aligned(16))) bf16 v_lds[2 * kVTile];
+  constexpr int STAGE = 2 * kTile;  // K tile then V^T tile
+  constexpr int LPW = 2 * kLoadsPerWave;
+  static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
   // logical workgroup: (b, kv head, head group) major, query block minor; the XCD remap keeps
   // the query blocks of one K/V head on one XCD so its K/V stay in that L2.
@@ -62,14 +74,14 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
   const int w = tid >> 6;
   const int group = p.heads / p.kv_heads;
   const int h = kvh * group + hg * p.hpw + (w % p.hpw);
-  const int q0 = qblk * p.rows_per_wg + (w / p.hpw) * 64;
+  const int q0 = qblk * p.rows_per_wg + (w / p.hpw) * 32 * QB;
   const long n_pad = p.n_pad;
 
   // Q fragments: B operand of S^T = K Q^T; lane holds query q0 + qb*32 + l32, dims s*16 + g*8 .. +8
   const bf16* qh = p.q + (static_cast<long>(b) * p.heads + h) * n_pad * kHd;
-  bf16x8 qf[2][8];
+  bf16x8 qf[QB][8];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const long row = min(static_cast<long>(q0 + qb * 32 + l32), n_pad - 1);
 #pragma unroll
     for (int s = 0; s < 8; ++s) qf[qb][s] = *reinterpret_cast<const bf16x8*>(qh + row * kHd + s * 16 + g * 8);
@@ -77,63 +89,72 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
 
   const bf16* kh = p.k + (static_cast<long>(b) * p.kv_heads + kvh) * n_pad * kHd;
   const bf16* vh = p.vt + (static_cast<long>(b) * p.kv_heads + kvh) * kHd * n_pad;
-
-  // per-thread fetch: 4 K chunks (key idx/16, dims 8*(idx%16)) and 4 V^T chunks (dim idx/8, keys 8*(idx%8))
-  bf16x8 kr[4], vr[4];
-  auto fetch = [&](int t) {
-    const long kv0 = static_cast<long>(t) * kKv;
+  // per-lane fetch offsets: K load j of wave w covers key rows 4 (4 w + j) .. +4 (16 chunks each),
+  // V^T load j covers dim rows 8 (4 w + j) .. +8 (8 chunks each)
+  int k_off[kLoadsPerWave], v_off[kLoadsPerWave];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i;
-      kr[i] = *reinterpret_cast<const bf16x8*>(kh + (kv0 + (idx >> 4)) * kHd + (idx & 15) * 8);
-      vr[i] = *reinterpret_cast<const bf16x8*>(vh + static_cast<long>(idx >> 3) * n_pad + kv0 + (idx & 7) * 8);
-    }
-  };
-  auto stash = [&](int buf) {
-    bf16* kl = k_lds + buf * kKTile;
-    bf16* vl = v_lds + buf * kVTile;
+  for (int j = 0; j < kLoadsPerWave; ++j) {
+    const int kr = (w * kLoadsPerWave + j) * 4 + (lane >> 4);
+    k_off[j] = kr * kHd + 8 * ((lane & 15) ^ (kr & 15));
+    const int vd = (w * kLoadsPerWave + j) * 8 + (lane >> 3);
+    v_off[j] = vd * static_cast<int>(n_pad) + 8 * ((lane & 7) ^ ((vd >> 1) & 7));
+  }
+  auto issue = [&](int t, int stage) {
+    bf16* kl = lds + stage * STAGE;
+    bf16* vl = kl + kTile;
+    const bf16* kt = kh + static_cast<long>(t) * kKv * kHd;
+    const bf16* vt = vh + static_cast<long>(t) * kKv;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i;
-      *reinterpret_cast<bf16x8*>(kl + (idx >> 4) * kKStride + (idx & 15) * 8) = kr[i];
-      // V^T rows are 136 bytes: 8-byte aligned only, so two 8-byte writes
-      bf16* dst = vl + (idx >> 3) * kVStride + (idx & 7) * 8;
-      *reinterpret_cast<bf16x4*>(dst) = bf16x4{vr[i][0], vr[i][1], vr[i][2], vr[i][3]};
-      *reinterpret_cast<bf16x4*>(dst + 4) = bf16x4{vr[i][4], vr[i][5], vr[i][6], vr[i][7]};
+    for (int j = 0; j < kLoadsPerWave; ++j) {
+      __builtin_amdgcn_global_load_lds((const void*)(kt + k_off[j]), (void*)(kl + (w * kLoadsPerWave + j) * 512), 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vt + v_off[j]), (void*)(vl + (w * kLoadsPerWave + j) * 512), 16,
+                                       0, 0);
     }
   };
 
-  f32x16 o[4][2];
+  f32x16 o[4][QB];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) o[db][0] = o[db][1] = f32x16{};
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.0f, 0.0f};
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) o[db][qb] = f32x16{};
+  float m_run[QB], l_run[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) m_run[qb] = -INFINITY, l_run[qb] = 0.0f;
   const float sl2 = p.scale_log2;
 
   const int n_tiles = (p.n + kKv - 1) / kKv;
-  fetch(0);
-  stash(0);
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < n_tiles) issue(s, s);
   for (int t = 0; t < n_tiles; ++t) {
-    const int cur = t & 1;
-    if (t + 1 < n_tiles) fetch(t + 1);
-    const bf16* kl = k_lds + cur * kKTile;
-    const bf16* vl = v_lds + cur * kVTile;
+    if (t + STAGES - 2 < n_tiles)
+      wait_vmcnt<(STAGES - 2) * LPW>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // tile t visible; stage (t-1) % STAGES no longer read
+    if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+    const bf16* kl = lds + (t % STAGES) * STAGE;
+    const bf16* vl = kl + kTile;
 
     // S^T[key, q] for keys kb*32 + (8 (r/4) + 4 g + r%4), queries qb*32 + l32
-    f32x16 s[2][2];
+    f32x16 s[2][QB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s[kb][0] = s[kb][1] = f32x16{};
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) s[kb][qb] = f32x16{};
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       bf16x8 kf[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-        kf[kb] = *reinterpret_cast<const bf16x8*>(kl + (kb * 32 + l32) * kKStride + st * 16 + g * 8);
+      for (int kb = 0; kb < 2; ++kb) {
+        const int r = kb * 32 + l32;
+        kf[kb] = *reinterpret_cast<const bf16x8*>(kl + r * kHd + 8 * ((2 * st + g) ^ (r & 15)));
+      }
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
           s[kb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[qb][st], s[kb][qb], 0, 0, 0);
     }
 
@@ -144,13 +165,15 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= p.n) s[kb][0][r] = s[kb][1][r] = -INFINITY;
+          if (key >= p.n)
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) s[kb][qb][r] = -INFINITY;
         }
     }
 
     // online softmax in the log2 domain, one query column per lane (and its partner lane ^ 32)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       float mx = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -180,32 +203,27 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        bf16x8 pf[2];
+        bf16x8 pf[QB];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
           for (int e = 0; e < 8; ++e) pf[qb][e] = from_f32<bf16>(s[kb][qb][8 * jj + e]);
-        const int off = kb * 32 + 16 * jj + 4 * g;
+        const int c = 4 * kb + 2 * jj + g;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          const bf16* vrow = vl + (db * 32 + l32) * kVStride + off;
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
-          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 8);
-          const bf16x8 vf = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const int d = db * 32 + l32;
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vl + d * kKv + 8 * (c ^ ((d >> 1) & 7)));
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
+          for (int qb = 0; qb < QB; ++qb)
             o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb], o[db][qb], 0, 0, 0);
         }
       }
     }
-
-    if (t + 1 < n_tiles) stash(cur ^ 1);
-    __syncthreads();
   }
 
   // epilogue: lane owns query q0 + qb*32 + l32 and dims db*32 + 8 j + 4 g + (0..3)
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const float l = l_run[qb] + __shfl_xor(l_run[qb], 32);
     const float inv = 1.0f / l;
     const int row = q0 + qb * 32 + l32;
@@ -236,6 +254,8 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
     }
   }
 }
+
+int g_attn_variant = -1;
 
 }  // namespace
 }  // namespace iris
@@ -280,14 +300,30 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   args.n = static_cast<int>(n);
   args.n_pad = static_cast<int>(n_pad);
   args.n_split = static_cast<int>(n_split);
+  // variant: 0 = 64 rows per wave, 2 stages; 1 = 64 rows, 3 stages; 2 = 32 rows, 2 stages
   args.hpw = group < 4 ? group : 4;
-  args.rows_per_wg = 64 * 4 / args.hpw;
+  const long wg64 = static_cast<long>(batch) * kv_heads * (group / args.hpw) * ((n + 64 * 4 / args.hpw - 1) / (64 * 4 / args.hpw));
+  const int variant = g_attn_variant >= 0 ? g_attn_variant : (wg64 >= 512 ? 1 : 2);
+  const int qb = variant == 2 ? 1 : 2;
+  args.rows_per_wg = 32 * qb * 4 / args.hpw;
   args.n_qblocks = static_cast<int>((n + args.rows_per_wg - 1) / args.rows_per_wg);
   args.n_hgroups = group / args.hpw;
   const long total = static_cast<long>(batch) * kv_heads * args.n_hgroups * args.n_qblocks;
   IRIS_REQUIRE(total < (1L << 31), "flash_attn: grid too large");
   args.total_wg = static_cast<int>(total);
   args.scale_log2 = scale * 1.4426950408889634f;
-  flash_attn_kernel<<<dim3(args.total_wg), 256, 0, stream>>>(args);
+  if (variant == 0)
+    flash_attn_kernel<2, 2><<<dim3(args.total_wg), 256, 0, stream>>>(args);
+  else if (variant == 1)
+    flash_attn_kernel<2, 3><<<dim3(args.total_wg), 256, 0, stream>>>(args);
+  else
+    flash_attn_kernel<1, 2><<<dim3(args.total_wg), 256, 0, stream>>>(args);
   return check_launch("flash_attn");
+}
+
+// Tuning hook: force an attention variant (0..2) or restore the automatic choice (-1).
+extern "C" int iris_flash_attn_force_variant(int variant) {
+  IRIS_REQUIRE(variant >= -1 && variant <= 2, "flash_attn_force_variant: variant in -1..2");
+  g_attn_variant = variant;
+  return IRIS_OK;
 }

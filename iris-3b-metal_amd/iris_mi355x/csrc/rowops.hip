@@ -133,43 +133,62 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict_
   store8(dst + ((b * heads + head) * n_dst + out_token) * 128 + 8 * sub, y);
 }
 
-// Transpose 64 tokens x 128 dims of one head into dst[b, h, d, token]. LDS rows are padded
-// by 8 elements (272 bytes) so the column reads of the second phase spread over the banks.
+// Position of token slot i inside its group of 16 in the V^T layout the attention kernel reads:
+// the middle two 4-token quads are swapped (0-3, 8-11, 4-7, 12-15), so that the 8 keys one
+// MFMA lane needs (4 g .. 4 g + 3 and 8 + 4 g .. 8 + 4 g + 3) are contiguous. An involution.
+__device__ __forceinline__ int vt_slot(int i) {
+  const int quad = (i >> 2) & 3;
+  return (i & ~15) | ((quad == 1 ? 2 : quad == 2 ? 1 : quad) << 2) | (i & 3);
+}
+
+// Transpose the V heads into dst[b, h, d, position]: one workgroup per (64 output positions
+// aligned to 64, head, batch). Position P holds token vt_slot(P) - dst_offset; LDS rows are
+// padded by 8 elements (272 bytes) so the column reads of the second phase spread over banks.
 __global__ __launch_bounds__(256) void v_heads_t_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst,
                                                         long n_src, long n_dst, int heads, long dst_offset,
                                                         long row_stride, long col_offset) {
   __shared__ bf16 tile[64][136];
-  const long t0 = static_cast<long>(blockIdx.x) * 64;
+  const long p0 = (dst_offset / 64 + blockIdx.x) * 64;  // first output position of the block
+  const long t0 = p0 - dst_offset;                       // token of position p0 (may be < 0)
   const int head = blockIdx.y;
   const long b = blockIdx.z;
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int idx = tid + 256 * i;  // 64 tokens x 16 chunks of 8
-    const int tok = idx >> 4;
+    const int idx = tid + 256 * i;  // 64 token slots x 16 chunks of 8
+    const int slot = idx >> 4;
     const int c = idx & 15;
+    const long tok = t0 + slot;
     bf16x8 v = {};
-    if (t0 + tok < n_src)
-      v = *reinterpret_cast<const bf16x8*>(src + (b * n_src + t0 + tok) * row_stride + col_offset + head * 128 +
-                                           8 * c);
-    *reinterpret_cast<bf16x8*>(&tile[tok][8 * c]) = v;
+    if (tok >= 0 && tok < n_src)
+      v = *reinterpret_cast<const bf16x8*>(src + (b * n_src + tok) * row_stride + col_offset + head * 128 + 8 * c);
+    *reinterpret_cast<bf16x8*>(&tile[slot][8 * c]) = v;
   }
   __syncthreads();
-  bf16* out = dst + (b * heads + head) * 128 * n_dst + dst_offset + t0;
+  bf16* out = dst + (b * heads + head) * 128 * n_dst + p0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int idx = tid + 256 * i;  // 128 dims x 8 chunks of 8 tokens
+    const int idx = tid + 256 * i;  // 128 dims x 8 chunks of 8 positions
     const int d = idx >> 3;
     const int c = idx & 7;
-    if (t0 + 8 * c >= n_src) continue;
     bf16x8 v;
+    int valid = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = tile[8 * c + e][d];
+    for (int e = 0; e < 8; ++e) {
+      const int slot = vt_slot(8 * c + e);
+      v[e] = tile[slot][d];
+      valid += (t0 + slot >= 0 && t0 + slot < n_src) ? 1 : 0;
+    }
+    if (valid == 0) continue;
     bf16* o = out + static_cast<long>(d) * n_dst + 8 * c;
-    if (t0 + 8 * c + 8 <= n_src && ((dst_offset + t0) & 7) == 0 && (n_dst & 7) == 0) {
+    if (valid == 8 && (n_dst & 7) == 0) {
       *reinterpret_cast<bf16x8*>(o) = v;
     } else {
-      for (int e = 0; e < 8 && t0 + 8 * c + e < n_src; ++e) o[e] = v[e];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int slot = vt_slot(8 * c + e);
+        if (t0 + slot >= 0 && t0 + slot < n_src) o[e] = v[e];
+      }
     }
   }
 }
@@ -325,10 +344,11 @@ extern "C" int iris_v_heads_t(const void* src, void* dst, int batch, long n_src,
                    col_offset % 8 == 0,
                "v_heads_t: heads must lie in 16-byte aligned rows of the projection");
   IRIS_REQUIRE(dst_offset >= 0 && dst_offset + n_src <= n_dst, "v_heads_t: output does not cover the rows");
+  IRIS_REQUIRE(n_dst % 64 == 0, "v_heads_t: the V^T rows must be a multiple of 64 positions");
   IRIS_REQUIRE(src && dst, "v_heads_t: null pointer");
   if (batch == 0 || n_src == 0) return IRIS_OK;
-  const dim3 grid(static_cast<unsigned>((n_src + 63) / 64), static_cast<unsigned>(heads),
-                  static_cast<unsigned>(batch));
+  const long first = dst_offset / 64, last = (dst_offset + n_src + 63) / 64;
+  const dim3 grid(static_cast<unsigned>(last - first), static_cast<unsigned>(heads), static_cast<unsigned>(batch));
   v_heads_t_kernel<<<grid, 256, 0, stream>>>((const bf16*)src, (bf16*)dst, n_src, n_dst, heads, dst_offset,
                                              row_stride, col_offset);
   return check_launch("v_heads_t");

@@ -215,9 +215,19 @@ def pixel_mlp_(
 # ---------------------------------------------------------------------------------------
 # kernels replacing the reference's PyTorch ops
 # ---------------------------------------------------------------------------------------
+def vt_positions(n: int) -> torch.Tensor:
+    """Token held by each of ``n`` positions of the V^T layout (quads 1 and 2 of every 16
+    positions swapped); the map is its own inverse."""
+    i = torch.arange(n)
+    quad = (i >> 2) & 3
+    swapped = torch.where(quad == 1, 2, torch.where(quad == 2, 1, quad))
+    return (i & ~15) | (swapped << 2) | (i & 3)
+
+
 def v_heads_t(x: torch.Tensor, heads: int, out: torch.Tensor, col_offset: int = 0, offset: int = 0) -> torch.Tensor:
     """Write the V heads at ``col_offset`` of a BF16 ``[B, N, W]`` projection into ``out``
-    (``[B, heads, 128, N_pad]``) transposed, at token columns ``offset + token``."""
+    (``[B, heads, 128, N_pad]``) transposed, token ``offset + t`` at position
+    ``vt_positions(N_pad)[offset + t]`` (the layout ``flash_attention`` reads)."""
     batch, tokens, width = x.shape
     _on_gpu(x, out)
     _require(x.dtype == torch.bfloat16 and out.dtype == torch.bfloat16, "v_heads_t works on BF16")

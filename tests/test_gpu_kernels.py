@@ -102,14 +102,26 @@ def test_qk_norm_rope_rejects_uncovered_rows():
         K.qk_norm_rope(x, w, cos, cos, 1e-6, 2)
 
 
-def test_v_heads_t_transposes_exactly():
-    b, n, heads = 2, 77, 5
+def test_vt_positions_is_the_quad_swap_involution():
+    pos = K.vt_positions(64)
+    assert pos[:16].tolist() == [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
+    assert torch.equal(pos[pos], torch.arange(64))
+
+
+@pytest.mark.parametrize("offset,n", [(16, 77), (0, 256), (37, 90)])
+def test_v_heads_t_writes_the_permuted_transpose(offset, n):
+    """Two projections (text rows, then image rows at an offset) land in one V^T buffer; every
+    position outside the written tokens keeps its previous value."""
+    b, heads, n_pad = 2, 5, 448
     x = torch.randn(b, n, 6400, generator=gen(4)).to(torch.bfloat16).to(DEV)
-    out = torch.zeros(b, heads, 128, 128, device=DEV, dtype=torch.bfloat16)
-    K.v_heads_t(x, heads, out, col_offset=3200, offset=16)
-    v = x[..., 3200:3200 + heads * 128].reshape(b, n, heads, 128).permute(0, 2, 3, 1)
-    assert torch.equal(out[..., 16:16 + n], v)
-    assert torch.all(out[..., :16] == 0) and torch.all(out[..., 16 + n:] == 0)
+    out = torch.full((b, heads, 128, n_pad), 3.0, device=DEV, dtype=torch.bfloat16)
+    K.v_heads_t(x, heads, out, col_offset=3200, offset=offset)
+    v = x[..., 3200:3200 + heads * 128].reshape(b, n, heads, 128).permute(0, 2, 3, 1).cpu()
+    token = K.vt_positions(n_pad) - offset  # token held by each position
+    got = out.cpu()
+    inside = (token >= 0) & (token < n)
+    assert torch.equal(got[..., inside], v[..., token[inside]])
+    assert torch.all(got[..., ~inside] == 3.0)
 
 
 # -- GEMM --------------------------------------------------------------------------------
@@ -177,7 +189,22 @@ def _attn_inputs(b, h, hkv, n, seed):
     kd = torch.zeros(b, hkv, n_pad, 128, dtype=torch.bfloat16)
     vt = torch.zeros(b, hkv, 128, n_pad, dtype=torch.bfloat16)
     qd[:, :, :n], kd[:, :, :n], vt[..., :n] = q, k, v.transpose(-1, -2)
+    vt = vt[..., K.vt_positions(n_pad)].contiguous()  # the kernel's V^T position order
     return q, k, v, qd.to(DEV), kd.to(DEV), vt.to(DEV)
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_flash_attention_variants(variant):
+    b, h, hkv, n = 1, 8, 2, 333
+    q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 16)
+    want = O.attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(b, n, h * 128)
+    out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+    _lib.call("iris_flash_attn_force_variant", variant)
+    try:
+        K.flash_attention(qd, kd, vt, n, None, out, n_split=0)
+    finally:
+        _lib.call("iris_flash_attn_force_variant", -1)
+    close_bf16(out.view(b, n, -1), want, scale=1.0, floor=4e-3)
 
 
 @pytest.mark.parametrize("b,h,hkv,n", [(1, 2, 1, 52), (2, 4, 1, 200), (1, 8, 2, 130), (1, 2, 2, 300)])
