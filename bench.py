@@ -143,20 +143,23 @@ def cpu_baseline(height: int, width: int, n_text: int, seed: int = 0) -> dict:
     text = torch.randn(1, n_text, D, generator=g)
     cond = torch.randn(1, 1, D, generator=g)
     img, txt, pix = O.rope_tables(cfg, grid, n_text)
+    tokens = torch.cat([text, s], dim=1)
+    pixels = torch.randn(L, p * p, cfg.pixel.hidden_size, generator=g)
+    cpix = torch.randn(L, D, generator=g)
+    blocks = {
+        "dual": lambda: O.mmdit_block(sd, cfg, 0, s, text, cond, img, txt),
+        "single": lambda: O.single_block(sd, cfg, 1, tokens, n_text, cond, img, txt),
+        "pixel": lambda: O.pit_block(sd, cfg, 0, pixels, cpix, pix, grid),
+    }
     times = {}
     with torch.no_grad():
-        t0 = time.perf_counter()
-        O.mmdit_block(sd, cfg, 0, s, text, cond, img, txt)
-        times["dual"] = time.perf_counter() - t0
-        tokens = torch.cat([text, s], dim=1)
-        t0 = time.perf_counter()
-        O.single_block(sd, cfg, 1, tokens, n_text, cond, img, txt)
-        times["single"] = time.perf_counter() - t0
-        pixels = torch.randn(L, p * p, cfg.pixel.hidden_size, generator=g)
-        cpix = torch.randn(L, D, generator=g)
-        t0 = time.perf_counter()
-        O.pit_block(sd, cfg, 0, pixels, cpix, pix, grid)
-        times["pixel"] = time.perf_counter() - t0
+        for name, fn in blocks.items():  # median of 3 runs per block kind
+            runs = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                fn()
+                runs.append(time.perf_counter() - t0)
+            times[name] = sorted(runs)[1]
     full = IRIS_3B
     n_dual = full.dual_depth
     step_s = n_dual * times["dual"] + (full.depth - n_dual) * times["single"] + full.pixel.depth * times["pixel"]
@@ -165,9 +168,10 @@ def cpu_baseline(height: int, width: int, n_text: int, seed: int = 0) -> dict:
         "unit": "steps/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"FP32 oracle, one dual ({times['dual']:.1f}s), one single ({times['single']:.1f}s) and one "
-                   f"pixel block ({times['pixel']:.1f}s) at {height}x{width}, {n_text} text tokens, composed as "
-                   f"{n_dual} dual + {full.depth - n_dual} single + {full.pixel.depth} pixel blocks per step"),
+        "sample": (f"FP32 oracle (torch CPU), median of 3 runs of one dual ({times['dual']:.2f}s), one single "
+                   f"({times['single']:.2f}s) and one pixel block ({times['pixel']:.2f}s) at {height}x{width}, "
+                   f"{n_text} text tokens, composed as {n_dual} dual + {full.depth - n_dual} single + "
+                   f"{full.pixel.depth} pixel blocks per step (embedders and head not counted)"),
     }
 
 

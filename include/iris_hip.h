@@ -48,6 +48,16 @@ int iris_gated_residual_rms_norm(float* residual, const void* branch, int branch
                                  const float* gate, long rows, long rows_per_batch, int width, long mod_stride,
                                  float eps, hipStream_t stream);
 
+/* iris_gated_residual_rms_norm followed by iris_rms_norm_modulate of the updated residual in one
+ * pass (the post-norm residual of one branch and the input norm of the next, model.py:286-289,
+ * 311-313): next_out[r] = (rmsnorm(residual[r]) * next_weight * (1 + next_scale[b]) + next_shift[b])
+ * in next_out_dtype, modulation rows next_mod_stride floats apart. */
+int iris_gated_residual_norm_modulate(float* residual, const void* branch, int branch_dtype, const float* weight,
+                                      const float* gate, long rows, long rows_per_batch, int width, long mod_stride,
+                                      float eps, const float* next_weight, const float* next_shift,
+                                      const float* next_scale, long next_mod_stride, void* next_out,
+                                      int next_out_dtype, hipStream_t stream);
+
 /* qk_norm_rope (src/iris_metal/kernels.py:37-84, wrapper 334-397): per (batch, token, head)
  * RMSNorm over 128 values with an FP32 gain, then rotation of pairs (2j, 2j+1) by
  * (cos, sin)[dst_offset + token, j]; reads heads at col_offset of a [batch, n_src, row_stride]

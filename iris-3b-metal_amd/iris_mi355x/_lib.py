@@ -25,6 +25,8 @@ _SIGNATURES: dict[str, list] = {
     "iris_abi_version": [],
     "iris_rms_norm_modulate": [P, c_int, P, c_int, P, P, P, c_long, c_long, c_int, c_long, c_float, P],
     "iris_gated_residual_rms_norm": [P, P, c_int, P, P, c_long, c_long, c_int, c_long, c_float, P],
+    "iris_gated_residual_norm_modulate": [P, P, c_int, P, P, c_long, c_long, c_int, c_long, c_float, P, P, P,
+                                          c_long, P, c_int, P],
     "iris_qk_norm_rope": [P, c_int, P, c_int, P, P, P, c_long, c_int, c_long, c_long, c_int, c_long, c_long,
                           c_long, c_float, P],
     "iris_v_heads_t": [P, P, c_int, c_long, c_long, c_int, c_long, c_long, c_long, P],

@@ -1,103 +1,173 @@
 // Row-wise bandwidth kernels of the trunk: RMSNorm + adaLN modulate, post-norm gated
-// residual, per-head qk-RMSNorm + 2-D RoPE, the V-head transpose, and small row utilities.
+// residual (optionally fused with the next RMSNorm + modulate), per-head qk-RMSNorm + 2-D
+// RoPE, the V-head transpose, and small row utilities.
 //
-// Layout: one 64-lane wave per row (token) for the D-wide row kernels, 16-byte vector
-// loads, the row cached in registers between the statistics pass and the output pass
-// so HBM sees each byte once.
+// Layout: one 64-lane wave per D-wide row; lane l owns the 8-element chunks l, l + 64, ...
+// (16-byte BF16 / 32-byte FP32 accesses, 1 KB or 2 KB contiguous per wave instruction), and
+// the row stays in registers between the statistics pass and the output pass, so HBM sees
+// each byte once.
 #include "iris_common.hpp"
 
 namespace iris {
 namespace {
 
-constexpr int kRowsPerBlock = 4;  // 4 waves = 4 rows per 256-thread workgroup
+constexpr int kRowsPerWave = 1;                   // rows a wave walks through
+constexpr int kRowsPerBlock = 4 * kRowsPerWave;    // 4 waves per 256-thread workgroup
 
-// NV = number of 4-element vectors each lane holds (width <= NV * 256).
-template <int NV, typename TI, typename TO>
+// NC = 8-element chunks each lane holds (width <= NC * 512). Every wave walks kRowsPerWave
+// consecutive rows and keeps the per-column coefficients (gain * (1 + scale), shift) in
+// registers while they stay in one batch: the FP32 vectors are read once per wave, not once
+// per row, so the kernel's L2 traffic stays close to its HBM traffic.
+template <int NC, typename TI, typename TO>
 __global__ __launch_bounds__(256) void rms_norm_modulate_kernel(const TI* __restrict__ x, TO* __restrict__ out,
                                                                 const float* __restrict__ weight,
                                                                 const float* __restrict__ shift,
                                                                 const float* __restrict__ scale, long rows,
                                                                 long rows_per_batch, int width, long mod_stride,
                                                                 float eps) {
-  const long row = static_cast<long>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  const long row0 = (static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
   const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const int nv = width >> 2;
-  const TI* xr = x + row * width;
-  f32x4 v[NV];
-  float ss = 0.0f;
+  const int nc = width >> 3;
+  float c1[NC][8], c0[NC][8];
+  long cur_b = -1;
+  for (int k = 0; k < kRowsPerWave; ++k) {
+    const long row = row0 + k;
+    if (row >= rows) return;
+    const long b = row / rows_per_batch;
+    if (b != cur_b) {  // wave-uniform
+      cur_b = b;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = lane + i * kWave;
-    if (j < nv) {
-      v[i] = load4(xr + 4 * j);
-      ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
-    }
-  }
-  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
-  const long b = row / rows_per_batch;
-  const float* sh = shift + b * mod_stride;
-  const float* sc = scale + b * mod_stride;
-  TO* o = out + row * width;
+      for (int i = 0; i < NC; ++i) {
+        const int j = lane + i * kWave;
+        if (j < nc) {
+          float w[8], s1[8];
+          load8(weight + 8 * j, w);
+          load8(scale + b * mod_stride + 8 * j, s1);
+          load8(shift + b * mod_stride + 8 * j, c0[i]);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = lane + i * kWave;
-    if (j < nv) {
-      const f32x4 w = load4(weight + 4 * j);
-      const f32x4 s1 = load4(sc + 4 * j);
-      const f32x4 s0 = load4(sh + 4 * j);
-      f32x4 y;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float h = (v[i][e] * r) * w[e];
-        y[e] = h * (1.0f + s1[e]) + s0[e];
+          for (int e = 0; e < 8; ++e) c1[i][e] = w[e] * (1.0f + s1[e]);
+        }
       }
-      store4(o + 4 * j, y);
+    }
+    const TI* xr = x + row * width;
+    float v[NC][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int j = lane + i * kWave;
+      if (j < nc) {
+        load8(xr + 8 * j, v[i]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+      }
+    }
+    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
+    TO* o = out + row * width;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int j = lane + i * kWave;
+      if (j < nc) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = (v[i][e] * r) * c1[i][e] + c0[i][e];
+        store8(o + 8 * j, y);
+      }
     }
   }
 }
 
-template <int NV, typename TB>
-__global__ __launch_bounds__(256) void gated_residual_kernel(float* __restrict__ residual,
-                                                             const TB* __restrict__ branch,
-                                                             const float* __restrict__ weight,
-                                                             const float* __restrict__ gate, long rows,
-                                                             long rows_per_batch, int width, long mod_stride,
-                                                             float eps) {
-  const long row = static_cast<long>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+// residual[r] += gate * rmsnorm(branch[r]) * weight; with next_out, also
+// next_out[r] = rmsnorm(residual[r]) * next_weight * (1 + next_scale) + next_shift from the
+// updated row still in registers (the next branch's input norm, without re-reading the row).
+// Coefficients (gate * weight, and next_weight * (1 + next_scale), next_shift) are held per
+// wave as in rms_norm_modulate_kernel.
+template <int NC, typename TB, typename TO>
+__global__ __launch_bounds__(256) void gated_residual_kernel(
+    float* __restrict__ residual, const TB* __restrict__ branch, const float* __restrict__ weight,
+    const float* __restrict__ gate, long rows, long rows_per_batch, int width, long mod_stride, float eps,
+    const float* __restrict__ next_weight, const float* __restrict__ next_shift,
+    const float* __restrict__ next_scale, long next_mod_stride, TO* __restrict__ next_out) {
+  const long row0 = (static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
   const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const int nv = width >> 2;
-  const TB* br = branch + row * width;
-  f32x4 v[NV];
-  float ss = 0.0f;
+  const int nc = width >> 3;
+  const bool fused = next_out != nullptr;
+  float gw[NC][8], c1[NC][8], c0[NC][8];
+  long cur_b = -1;
+  for (int k = 0; k < kRowsPerWave; ++k) {
+    const long row = row0 + k;
+    if (row >= rows) return;
+    const long b = row / rows_per_batch;
+    if (b != cur_b) {  // wave-uniform
+      cur_b = b;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = lane + i * kWave;
-    if (j < nv) {
-      v[i] = load4(br + 4 * j);
-      ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+      for (int i = 0; i < NC; ++i) {
+        const int j = lane + i * kWave;
+        if (j < nc) {
+          float w[8], g[8];
+          load8(weight + 8 * j, w);
+          load8(gate + b * mod_stride + 8 * j, g);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) gw[i][e] = g[e] * w[e];
+          if (fused) {
+            float w2[8], s1[8];
+            load8(next_weight + 8 * j, w2);
+            load8(next_scale + b * next_mod_stride + 8 * j, s1);
+            load8(next_shift + b * next_mod_stride + 8 * j, c0[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) c1[i][e] = w2[e] * (1.0f + s1[e]);
+          }
+        }
+      }
     }
-  }
-  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
-  const float* g = gate + (row / rows_per_batch) * mod_stride;
-  float* res = residual + row * width;
+    const TB* br = branch + row * width;
+    float* res = residual + row * width;
+    float v[NC][8], x[NC][8];
+    float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = lane + i * kWave;
-    if (j < nv) {
-      const f32x4 w = load4(weight + 4 * j);
-      const f32x4 gv = load4(g + 4 * j);
-      f32x4 acc = load4(res + 4 * j);
+    for (int i = 0; i < NC; ++i) {
+      const int j = lane + i * kWave;
+      if (j < nc) {
+        load8(br + 8 * j, v[i]);
+        load8(res + 8 * j, x[i]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] += gv[e] * ((v[i][e] * r) * w[e]);
-      store4(res + 4 * j, acc);
+        for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+      }
+    }
+    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
+    float ss2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int j = lane + i * kWave;
+      if (j < nc) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[i][e] += gw[i][e] * (v[i][e] * r);
+          ss2 += x[i][e] * x[i][e];
+        }
+        store8(res + 8 * j, x[i]);
+      }
+    }
+    if (!fused) continue;
+    const float r2 = rsqrtf(wave_sum(ss2) / static_cast<float>(width) + eps);
+    TO* o = next_out + row * width;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int j = lane + i * kWave;
+      if (j < nc) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = (x[i][e] * r2) * c1[i][e] + c0[i][e];
+        store8(o + 8 * j, y);
+      }
     }
   }
 }
 
 // 16 lanes per (token, head) row of 128 values; lane s owns elements [8s, 8s+8) = rotary
-// pairs 4s..4s+3. Four rows per wave, sixteen per workgroup.
+// pairs 4s..4s+3. A 16-lane group handles up to kQkRows heads of one token (all loads issued
+// before the first reduction, the token's rotary row read once), 16 groups per workgroup.
+constexpr int kQkRows = 4;
+
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict__ src, TO* __restrict__ dst,
                                                            const float* __restrict__ weight,
@@ -105,32 +175,41 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict_
                                                            const float* __restrict__ sin_table, long n_src,
                                                            long n_dst, int heads, long dst_offset, long row_stride,
                                                            long col_offset, float eps) {
-  const long row = static_cast<long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  // group = (token, up to kQkRows consecutive heads): the rotary row is read once per group
+  const int head_groups = (heads + kQkRows - 1) / kQkRows;
+  const long grp = static_cast<long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   const long b = blockIdx.y;
-  if (row >= n_src * heads) return;  // whole 16-lane groups leave together
-  const long token = row / heads;
-  const int head = static_cast<int>(row - token * heads);
-  float a[8];
-  load8(src + (b * n_src + token) * row_stride + col_offset + head * 128 + 8 * sub, a);
-  float ss = 0.0f;
+  if (grp >= n_src * head_groups) return;  // whole 16-lane groups leave together
+  const long token = grp / head_groups;
+  const int head0 = static_cast<int>(grp - token * head_groups) * kQkRows;
+  const TI* xr = src + (b * n_src + token) * row_stride + col_offset + 8 * sub;
+  float a[kQkRows][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss += a[e] * a[e];
-  const float r = rsqrtf(group_sum<16>(ss) / 128.0f + eps);
+  for (int k = 0; k < kQkRows; ++k) load8(xr + min(head0 + k, heads - 1) * 128, a[k]);
   float w[8];
   load8(weight + 8 * sub, w);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) a[e] = (a[e] * r) * w[e];
   const long out_token = dst_offset + token;
   const f32x4 c = load4(cos_table + out_token * 64 + 4 * sub);
   const f32x4 s = load4(sin_table + out_token * 64 + 4 * sub);
-  float y[8];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    y[2 * p] = a[2 * p] * c[p] - a[2 * p + 1] * s[p];
-    y[2 * p + 1] = a[2 * p] * s[p] + a[2 * p + 1] * c[p];
+  for (int k = 0; k < kQkRows; ++k) {
+    const int head = head0 + k;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += a[k][e] * a[k][e];
+    const float r = rsqrtf(group_sum<16>(ss) / 128.0f + eps);
+    if (head >= heads) continue;
+    float y[8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float a0 = (a[k][2 * p] * r) * w[2 * p];
+      const float a1 = (a[k][2 * p + 1] * r) * w[2 * p + 1];
+      y[2 * p] = a0 * c[p] - a1 * s[p];
+      y[2 * p + 1] = a0 * s[p] + a1 * c[p];
+    }
+    store8(dst + ((b * heads + head) * n_dst + out_token) * 128 + 8 * sub, y);
   }
-  store8(dst + ((b * heads + head) * n_dst + out_token) * 128 + 8 * sub, y);
 }
 
 // Position of token slot i inside its group of 16 in the V^T layout the attention kernel reads:
@@ -224,29 +303,68 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const float* __restrict_
          load4(src + (b * src_batch_rows + src_row_offset + row) * width + col));
 }
 
-int nv_bucket(int width) {
-  const int need = (width / 4 + kWave - 1) / kWave;
+int nc_bucket(int width) {
+  const int need = (width / 8 + kWave - 1) / kWave;
   if (need <= 1) return 1;
   if (need <= 2) return 2;
-  if (need <= 4) return 4;
+  if (need <= 3) return 3;
+  if (need <= 5) return 5;
   if (need <= 8) return 8;
-  if (need <= 10) return 10;
-  if (need <= 16) return 16;
-  return 32;
+  return 16;
 }
 
-#define IRIS_NV_DISPATCH(NVV, ...)              \
-  switch (NVV) {                                \
-    case 1: { constexpr int NV = 1; __VA_ARGS__; } break;   \
-    case 2: { constexpr int NV = 2; __VA_ARGS__; } break;   \
-    case 4: { constexpr int NV = 4; __VA_ARGS__; } break;   \
-    case 8: { constexpr int NV = 8; __VA_ARGS__; } break;   \
-    case 10: { constexpr int NV = 10; __VA_ARGS__; } break; \
-    case 16: { constexpr int NV = 16; __VA_ARGS__; } break; \
-    default: { constexpr int NV = 32; __VA_ARGS__; } break; \
+#define IRIS_NC_DISPATCH(NCV, ...)                          \
+  switch (NCV) {                                            \
+    case 1: { constexpr int NC = 1; __VA_ARGS__; } break;   \
+    case 2: { constexpr int NC = 2; __VA_ARGS__; } break;   \
+    case 3: { constexpr int NC = 3; __VA_ARGS__; } break;   \
+    case 5: { constexpr int NC = 5; __VA_ARGS__; } break;   \
+    case 8: { constexpr int NC = 8; __VA_ARGS__; } break;   \
+    default: { constexpr int NC = 16; __VA_ARGS__; } break; \
   }
 
 bool valid_dtype(int dt) { return dt == IRIS_F32 || dt == IRIS_BF16; }
+
+template <int NC, typename TB>
+void launch_gated(dim3 grid, hipStream_t stream, float* residual, const void* branch, const float* weight,
+                  const float* gate, long rows, long rows_per_batch, int width, long mod_stride, float eps,
+                  const float* nw, const float* nsh, const float* nsc, long nstride, void* next_out, int out_dtype) {
+  if (out_dtype == IRIS_F32)
+    gated_residual_kernel<NC, TB, float><<<grid, 256, 0, stream>>>(residual, (const TB*)branch, weight, gate, rows,
+                                                                   rows_per_batch, width, mod_stride, eps, nw, nsh,
+                                                                   nsc, nstride, (float*)next_out);
+  else
+    gated_residual_kernel<NC, TB, bf16><<<grid, 256, 0, stream>>>(residual, (const TB*)branch, weight, gate, rows,
+                                                                  rows_per_batch, width, mod_stride, eps, nw, nsh,
+                                                                  nsc, nstride, (bf16*)next_out);
+}
+
+int gated_common(float* residual, const void* branch, int branch_dtype, const float* weight, const float* gate,
+                 long rows, long rows_per_batch, int width, long mod_stride, float eps, const float* nw,
+                 const float* nsh, const float* nsc, long nstride, void* next_out, int out_dtype,
+                 hipStream_t stream) {
+  IRIS_REQUIRE(valid_dtype(branch_dtype) && valid_dtype(out_dtype), "gated_residual_rms_norm: unknown dtype");
+  IRIS_REQUIRE(width > 0 && width % 128 == 0 && width <= 8192,
+               "gated_residual_rms_norm_ shape mismatch: width %% 128 == 0 and <= 8192 (got %d)", width);
+  IRIS_REQUIRE(rows >= 0 && rows_per_batch > 0, "gated_residual_rms_norm: bad row counts");
+  IRIS_REQUIRE(mod_stride % 4 == 0 && aligned(gate, 16) && aligned(weight, 16),
+               "gated_residual_rms_norm: gate rows must be 16-byte aligned");
+  IRIS_REQUIRE(residual && branch && weight && gate, "gated_residual_rms_norm: null pointer");
+  IRIS_REQUIRE(!next_out || (nw && nsh && nsc && nstride % 4 == 0 && aligned(nw, 16) && aligned(nsh, 16) &&
+                             aligned(nsc, 16)),
+               "gated_residual_rms_norm: the next norm needs 16-byte aligned FP32 gain and modulation rows");
+  if (rows == 0) return IRIS_OK;
+  const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  IRIS_NC_DISPATCH(nc_bucket(width), {
+    if (branch_dtype == IRIS_BF16)
+      launch_gated<NC, bf16>(grid, stream, residual, branch, weight, gate, rows, rows_per_batch, width, mod_stride,
+                             eps, nw, nsh, nsc, nstride, next_out, out_dtype);
+    else
+      launch_gated<NC, float>(grid, stream, residual, branch, weight, gate, rows, rows_per_batch, width,
+                              mod_stride, eps, nw, nsh, nsc, nstride, next_out, out_dtype);
+  })
+  return check_launch("gated_residual_rms_norm");
+}
 
 }  // namespace
 }  // namespace iris
@@ -265,18 +383,18 @@ extern "C" int iris_rms_norm_modulate(const void* x, int x_dtype, void* out, int
   IRIS_REQUIRE(x && out && weight && shift && scale, "rms_norm_modulate: null pointer");
   if (rows == 0) return IRIS_OK;
   const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
-  IRIS_NV_DISPATCH(nv_bucket(width), {
+  IRIS_NC_DISPATCH(nc_bucket(width), {
     if (x_dtype == IRIS_F32 && out_dtype == IRIS_BF16)
-      rms_norm_modulate_kernel<NV, float, bf16><<<grid, 256, 0, stream>>>(
+      rms_norm_modulate_kernel<NC, float, bf16><<<grid, 256, 0, stream>>>(
           (const float*)x, (bf16*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
     else if (x_dtype == IRIS_F32 && out_dtype == IRIS_F32)
-      rms_norm_modulate_kernel<NV, float, float><<<grid, 256, 0, stream>>>(
+      rms_norm_modulate_kernel<NC, float, float><<<grid, 256, 0, stream>>>(
           (const float*)x, (float*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
     else if (x_dtype == IRIS_BF16 && out_dtype == IRIS_BF16)
-      rms_norm_modulate_kernel<NV, bf16, bf16><<<grid, 256, 0, stream>>>(
+      rms_norm_modulate_kernel<NC, bf16, bf16><<<grid, 256, 0, stream>>>(
           (const bf16*)x, (bf16*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
     else
-      rms_norm_modulate_kernel<NV, bf16, float><<<grid, 256, 0, stream>>>(
+      rms_norm_modulate_kernel<NC, bf16, float><<<grid, 256, 0, stream>>>(
           (const bf16*)x, (float*)out, weight, shift, scale, rows, rows_per_batch, width, mod_stride, eps);
   })
   return check_launch("rms_norm_modulate");
@@ -285,24 +403,19 @@ extern "C" int iris_rms_norm_modulate(const void* x, int x_dtype, void* out, int
 extern "C" int iris_gated_residual_rms_norm(float* residual, const void* branch, int branch_dtype,
                                             const float* weight, const float* gate, long rows, long rows_per_batch,
                                             int width, long mod_stride, float eps, hipStream_t stream) {
-  IRIS_REQUIRE(valid_dtype(branch_dtype), "gated_residual_rms_norm: unknown dtype");
-  IRIS_REQUIRE(width > 0 && width % 128 == 0 && width <= 8192,
-               "gated_residual_rms_norm_ shape mismatch: width %% 128 == 0 and <= 8192 (got %d)", width);
-  IRIS_REQUIRE(rows >= 0 && rows_per_batch > 0, "gated_residual_rms_norm: bad row counts");
-  IRIS_REQUIRE(mod_stride % 4 == 0 && aligned(gate, 16) && aligned(weight, 16),
-               "gated_residual_rms_norm: gate rows must be 16-byte aligned");
-  IRIS_REQUIRE(residual && branch && weight && gate, "gated_residual_rms_norm: null pointer");
-  if (rows == 0) return IRIS_OK;
-  const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
-  IRIS_NV_DISPATCH(nv_bucket(width), {
-    if (branch_dtype == IRIS_BF16)
-      gated_residual_kernel<NV, bf16><<<grid, 256, 0, stream>>>(residual, (const bf16*)branch, weight, gate, rows,
-                                                                rows_per_batch, width, mod_stride, eps);
-    else
-      gated_residual_kernel<NV, float><<<grid, 256, 0, stream>>>(residual, (const float*)branch, weight, gate,
-                                                                 rows, rows_per_batch, width, mod_stride, eps);
-  })
-  return check_launch("gated_residual_rms_norm");
+  return gated_common(residual, branch, branch_dtype, weight, gate, rows, rows_per_batch, width, mod_stride, eps,
+                      nullptr, nullptr, nullptr, 0, nullptr, IRIS_BF16, stream);
+}
+
+extern "C" int iris_gated_residual_norm_modulate(float* residual, const void* branch, int branch_dtype,
+                                                 const float* weight, const float* gate, long rows,
+                                                 long rows_per_batch, int width, long mod_stride, float eps,
+                                                 const float* next_weight, const float* next_shift,
+                                                 const float* next_scale, long next_mod_stride, void* next_out,
+                                                 int next_out_dtype, hipStream_t stream) {
+  IRIS_REQUIRE(next_out != nullptr, "gated_residual_norm_modulate: next_out is required");
+  return gated_common(residual, branch, branch_dtype, weight, gate, rows, rows_per_batch, width, mod_stride, eps,
+                      next_weight, next_shift, next_scale, next_mod_stride, next_out, next_out_dtype, stream);
 }
 
 extern "C" int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int dst_dtype, const float* weight,
@@ -311,7 +424,7 @@ extern "C" int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int 
                                  long col_offset, float eps, hipStream_t stream) {
   IRIS_REQUIRE(valid_dtype(src_dtype) && valid_dtype(dst_dtype), "qk_norm_rope: unknown dtype");
   IRIS_REQUIRE(heads > 0 && col_offset >= 0 && dst_offset >= 0, "heads must be positive and offsets nonnegative");
-  IRIS_REQUIRE(batch >= 0 && n_src >= 0, "qk_norm_rope: bad sizes");
+  IRIS_REQUIRE(batch >= 0 && batch <= 65535 && n_src >= 0, "qk_norm_rope: bad sizes");
   IRIS_REQUIRE(col_offset + heads * 128L <= row_stride,
                "qk_norm_rope needs a contiguous [B, N, W] input holding the heads");
   IRIS_REQUIRE(dst_offset + n_src <= table_rows && dst_offset + n_src <= n_dst,
@@ -319,7 +432,8 @@ extern "C" int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int 
   IRIS_REQUIRE(row_stride % 8 == 0 && col_offset % 8 == 0, "qk_norm_rope: rows must be 16-byte aligned");
   IRIS_REQUIRE(src && dst && weight && cos_table && sin_table, "qk_norm_rope: null pointer");
   if (batch == 0 || n_src == 0) return IRIS_OK;
-  const dim3 grid(static_cast<unsigned>((n_src * heads + 15) / 16), static_cast<unsigned>(batch));
+  const long groups = n_src * ((heads + kQkRows - 1) / kQkRows);  // (token, head group) pairs
+  const dim3 grid(static_cast<unsigned>((groups + 15) / 16), static_cast<unsigned>(batch));
 #define IRIS_QK_LAUNCH(TI, TO)                                                                                   \
   qk_norm_rope_kernel<TI, TO><<<grid, 256, 0, stream>>>((const TI*)src, (TO*)dst, weight, cos_table, sin_table, \
                                                         n_src, n_dst, heads, dst_offset, row_stride, col_offset, \

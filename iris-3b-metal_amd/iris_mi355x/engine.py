@@ -297,15 +297,20 @@ class HipIris:
         Y = ws["Y"]
         K.copy_rows(text.reshape(B * T, D), Y, B, T, 0, T, 0, T)
         joined = False
+        h_ready = False  # the next block's input norms were produced by the previous block
         for i, blk in enumerate(self.blocks):
+            nxt = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
             if blk["kind"] == "mmdit":
-                self._dual_block(ws, blk, B, T, Lp, N)
+                fuse = nxt is not None and nxt["kind"] == "mmdit"
+                self._dual_block(ws, blk, B, T, Lp, N, h_ready, nxt if fuse else None)
+                h_ready = fuse
                 continue
             if not joined:
                 K.copy_rows(Y, ws["tok"], B, T, 0, T, 0, N)
                 K.copy_rows(ws["X"], ws["tok"], B, Lp, 0, Lp, T, N)
                 joined = True
-            self._single_block(ws, blk, B, T, Lp, N, last=i == cfg.depth - 1)
+            self._single_block(ws, blk, B, T, Lp, N, i == cfg.depth - 1, h_ready, nxt)
+            h_ready = nxt is not None
 
         # pixel stage
         K.silu_add_rows(ws["X"], ws["temb"], Lp, ws["scond"])
@@ -318,13 +323,16 @@ class HipIris:
         D = self.cfg.hidden_size
         return ws[table][index][:, chunk * D:(chunk + 1) * D].unsqueeze(1)
 
-    def _dual_block(self, ws: dict, blk: dict, B: int, T: int, Lp: int, N: int) -> None:
+    def _dual_block(self, ws: dict, blk: dict, B: int, T: int, Lp: int, N: int, h_ready: bool,
+                    nxt: dict | None) -> None:
+        """One dual-stream block on the image ``X`` and text ``Y`` residuals. With ``h_ready`` the
+        input norms are already in the ``h`` rows (fused into the previous block's last residual);
+        with ``nxt`` (a dual block) this block's last residual also produces ``nxt``'s input norms."""
         cfg, eps = self.cfg, self.eps
         D, H, Hkv = cfg.hidden_size, cfg.num_heads, cfg.kv_heads
-        X, Y = ws["X"], ws["Y"]
-        mi, mt = blk["img_mod"], blk["txt_mod"]
-        xm = [self._mods(ws, "mods_img", mi, c) for c in range(6)]
-        ym = [self._mods(ws, "mods_txt", mt, c) for c in range(6)]
+        X, Y = ws["X"].view(B, Lp, D), ws["Y"].view(B, T, D)
+        xm = [self._mods(ws, "mods_img", blk["img_mod"], c) for c in range(6)]
+        ym = [self._mods(ws, "mods_txt", blk["txt_mod"], c) for c in range(6)]
         qkvg_w = ws["qkvg"].shape[1]
         rows_x, rows_y = B * Lp, B * T
         hx, hy = ws["h_tok"][:rows_x], ws["h_tok"][rows_x:rows_x + rows_y]
@@ -332,9 +340,11 @@ class HipIris:
         ax, ay = ws["attn"][:rows_x], ws["attn"][rows_x:rows_x + rows_y]
         bx, by = ws["branch"][:rows_x], ws["branch"][rows_x:rows_x + rows_y]
         hhx, hhy = ws["hh"][:rows_x], ws["hh"][rows_x:rows_x + rows_y]
+        bf16 = torch.bfloat16
 
-        K.rms_norm_modulate(X.view(B, Lp, D), blk["norm_x1"], xm[0], xm[1], eps, torch.bfloat16, out=hx.view(B, Lp, D))
-        K.rms_norm_modulate(Y.view(B, T, D), blk["norm_y1"], ym[0], ym[1], eps, torch.bfloat16, out=hy.view(B, T, D))
+        if not h_ready:
+            K.rms_norm_modulate(X, blk["norm_x1"], xm[0], xm[1], eps, bf16, out=hx.view(B, Lp, D))
+            K.rms_norm_modulate(Y, blk["norm_y1"], ym[0], ym[1], eps, bf16, out=hy.view(B, T, D))
         K.linear_grouped([hx, hy], [blk["qkvg_x"], blk["qkvg_y"]], None, [px, py])
         rope_c, rope_s = ws["rope"]
         q, k, vt = ws["q"], ws["k"], ws["vt"]
@@ -346,16 +356,27 @@ class HipIris:
         gate_col = (H + 2 * Hkv) * HEAD_DIM
         K.flash_attention(q, k, vt, N, ay, ax, n_split=T, gate0=py[:, gate_col:], gate1=px[:, gate_col:])
         K.linear_grouped([ax, ay], [blk["proj_x_w"], blk["proj_y_w"]], [blk["proj_x_b"], blk["proj_y_b"]], [bx, by])
-        K.gated_residual_rms_norm_(X.view(B, Lp, D), bx.view(B, Lp, D), blk["attn_post_norm_x"], xm[2], eps)
-        K.gated_residual_rms_norm_(Y.view(B, T, D), by.view(B, T, D), blk["attn_post_norm_y"], ym[2], eps)
-        K.rms_norm_modulate(X.view(B, Lp, D), blk["norm_x2"], xm[3], xm[4], eps, torch.bfloat16, out=hx.view(B, Lp, D))
-        K.rms_norm_modulate(Y.view(B, T, D), blk["norm_y2"], ym[3], ym[4], eps, torch.bfloat16, out=hy.view(B, T, D))
+        K.gated_residual_norm_modulate_(X, bx.view(B, Lp, D), blk["attn_post_norm_x"], xm[2], eps,
+                                        blk["norm_x2"], xm[3], xm[4], hx.view(B, Lp, D))
+        K.gated_residual_norm_modulate_(Y, by.view(B, T, D), blk["attn_post_norm_y"], ym[2], eps,
+                                        blk["norm_y2"], ym[3], ym[4], hy.view(B, T, D))
         K.linear_grouped([hx, hy], [blk["w13_x"], blk["w13_y"]], None, [hhx, hhy], swiglu=True)
         K.linear_grouped([hhx, hhy], [blk["w2_x"], blk["w2_y"]], None, [bx, by])
-        K.gated_residual_rms_norm_(X.view(B, Lp, D), bx.view(B, Lp, D), blk["mlp_post_norm_x"], xm[5], eps)
-        K.gated_residual_rms_norm_(Y.view(B, T, D), by.view(B, T, D), blk["mlp_post_norm_y"], ym[5], eps)
+        if nxt is None:
+            K.gated_residual_rms_norm_(X, bx.view(B, Lp, D), blk["mlp_post_norm_x"], xm[5], eps)
+            K.gated_residual_rms_norm_(Y, by.view(B, T, D), blk["mlp_post_norm_y"], ym[5], eps)
+        else:
+            nx = [self._mods(ws, "mods_img", nxt["img_mod"], c) for c in range(2)]
+            ny = [self._mods(ws, "mods_txt", nxt["txt_mod"], c) for c in range(2)]
+            K.gated_residual_norm_modulate_(X, bx.view(B, Lp, D), blk["mlp_post_norm_x"], xm[5], eps,
+                                            nxt["norm_x1"], nx[0], nx[1], hx.view(B, Lp, D))
+            K.gated_residual_norm_modulate_(Y, by.view(B, T, D), blk["mlp_post_norm_y"], ym[5], eps,
+                                            nxt["norm_y1"], ny[0], ny[1], hy.view(B, T, D))
 
-    def _single_block(self, ws: dict, blk: dict, B: int, T: int, Lp: int, N: int, last: bool) -> None:
+    def _single_block(self, ws: dict, blk: dict, B: int, T: int, Lp: int, N: int, last: bool, h_ready: bool,
+                      nxt: dict | None) -> None:
+        """One single-stream block on ``tok`` (the last one continues on the image rows only).
+        ``h_ready`` / ``nxt``: as for ``_dual_block``, with ``nxt`` a single-stream block."""
         cfg, eps = self.cfg, self.eps
         D, H, Hkv = cfg.hidden_size, cfg.num_heads, cfg.kv_heads
         tok = ws["tok"]
@@ -363,7 +384,8 @@ class HipIris:
         rows = B * N
         h, proj = ws["h_tok"][:rows], ws["qkvg"][:rows]
         qkvg_w = proj.shape[1]
-        K.rms_norm_modulate(tok.view(B, N, D), blk["norm1"], m[0], m[1], eps, torch.bfloat16, out=h.view(B, N, D))
+        if not h_ready:
+            K.rms_norm_modulate(tok.view(B, N, D), blk["norm1"], m[0], m[1], eps, torch.bfloat16, out=h.view(B, N, D))
         K.linear(h, blk["qkvg"], out=proj)
         rope_c, rope_s = ws["rope"]
         pv = proj.view(B, N, qkvg_w)
@@ -385,15 +407,18 @@ class HipIris:
                               out_batch_rows=(T, Lp), gate_batch_rows=(T, N))
         branch, hh = ws["branch"][:M], ws["hh"][:M]
         h2 = ws["h_tok"][:M]
+        Rv = R.view(B, per_batch, D)
         K.linear(attn, blk["proj_w"], blk["proj_b"], out=branch)
-        K.gated_residual_rms_norm_(R.view(B, per_batch, D), branch.view(B, per_batch, D), blk["attn_post_norm"],
-                                   m[2], eps)
-        K.rms_norm_modulate(R.view(B, per_batch, D), blk["norm2"], m[3], m[4], eps, torch.bfloat16,
-                            out=h2.view(B, per_batch, D))
+        K.gated_residual_norm_modulate_(Rv, branch.view(B, per_batch, D), blk["attn_post_norm"], m[2], eps,
+                                        blk["norm2"], m[3], m[4], h2.view(B, per_batch, D))
         K.linear(h2, blk["w13"], out=hh, swiglu=True)
         K.linear(hh, blk["w2"], out=branch)
-        K.gated_residual_rms_norm_(R.view(B, per_batch, D), branch.view(B, per_batch, D), blk["mlp_post_norm"],
-                                   m[5], eps)
+        if nxt is None:
+            K.gated_residual_rms_norm_(Rv, branch.view(B, per_batch, D), blk["mlp_post_norm"], m[5], eps)
+        else:
+            n1 = [self._mods(ws, "mods_img", nxt["img_mod"], c) for c in range(2)]
+            K.gated_residual_norm_modulate_(Rv, branch.view(B, per_batch, D), blk["mlp_post_norm"], m[5], eps,
+                                            nxt["norm1"], n1[0], n1[1], h.view(B, N, D))
 
     def _pixel_block(self, ws: dict, blk: dict, B: int, Lp: int, next_norm: torch.Tensor) -> None:
         cfg, eps = self.cfg, self.eps

@@ -143,6 +143,33 @@ def gated_residual_rms_norm_(
     return residual
 
 
+def gated_residual_norm_modulate_(
+    residual: torch.Tensor, branch: torch.Tensor, weight: torch.Tensor, gate: torch.Tensor, eps: float,
+    next_weight: torch.Tensor, next_shift: torch.Tensor, next_scale: torch.Tensor, out: torch.Tensor,
+) -> torch.Tensor:
+    """``gated_residual_rms_norm_`` then ``rms_norm_modulate`` of the updated residual into ``out``,
+    in one pass over the row (the residual is read and written once)."""
+    batch, tokens, width = residual.shape
+    _on_gpu(residual, branch, weight, gate, next_weight, next_shift, next_scale, out)
+    _require(width % 128 == 0 and branch.shape == residual.shape, "gated_residual_rms_norm_ shape mismatch")
+    _require(branch.is_contiguous() and out.is_contiguous() and out.shape == residual.shape,
+             "gated_residual_norm_modulate_ needs contiguous branch and output")
+    _require_fp32(residual=residual, weight=weight, next_weight=next_weight)
+    _require(weight.numel() == next_weight.numel() == width, "gated_residual_norm_modulate_ gain width mismatch")
+    gate, gate_stride = _per_batch(gate, batch, width)
+    shift, shift_stride = _per_batch(next_shift, batch, width)
+    scale, scale_stride = _per_batch(next_scale, batch, width)
+    if shift_stride != scale_stride:
+        shift, scale = shift.contiguous(), scale.contiguous()
+        shift_stride = width
+    L.call(
+        "iris_gated_residual_norm_modulate", L.ptr(residual), L.ptr(branch), L.dtype_code(branch.dtype),
+        L.ptr(weight), L.ptr(gate), batch * tokens, tokens, width, gate_stride, float(eps), L.ptr(next_weight),
+        L.ptr(shift), L.ptr(scale), shift_stride, L.ptr(out), L.dtype_code(out.dtype), L.stream(),
+    )
+    return out
+
+
 def pixel_rms_norm(pixels: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """``rms_norm(pixels) * weight`` over the 16 channels of each pixel, stored BF16
     (src/iris_metal/kernels.py:486-498)."""

@@ -1,0 +1,184 @@
+"""Kernel microbenchmarks of libiris_hip.so (one GPU), also used as rocprofv3 drivers.
+
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench fused-ops
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench gemm 4352 6400 2560
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench attention 1 20 5 4352
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench copy 1
+
+``fused-ops`` is the bandwidth microbenchmark of the row kernels at the single-stream block
+shape [1, 4352, 2560] BF16: RMSNorm + adaLN modulate, per-head qk-RMSNorm + 2-D RoPE for Q
+(20 heads) and K (5 heads), and the post-norm gated residual. Inputs are N(0, 1), modulation
+vectors N(0, 0.1), gains 1 + N(0, 0.02); each timed call uses the next of several buffer sets
+whose total exceeds the 256 MB Infinity Cache, and GB/s counts the algorithmic bytes (every
+input read once, every output written once). Times come from HIP events on the launch stream.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+
+import torch
+
+from . import _lib
+from . import kernels as K
+from . import tables
+
+HBM_GBS = 8000.0
+MFMA_TFLOPS = 2500.0
+
+
+def _time(fn, iters: int, warmup: int = 3) -> float:
+    """Average milliseconds per call of ``fn(i)`` over ``iters`` calls (HIP events)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def _sets(nbytes_per_set: int, floor: int = 4, cache_bytes: int = 256 << 20) -> int:
+    return max(floor, -(-2 * cache_bytes // nbytes_per_set))
+
+
+def fused_ops(iters: int = 50) -> list[dict]:
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    n, d, heads, kv_heads, eps = 4352, 2560, 20, 5, 1e-6
+    results = []
+
+    def randn(*shape, scale=1.0, dtype=torch.bfloat16):
+        return (scale * torch.randn(*shape, generator=g, device=dev)).to(dtype)
+
+    # RMSNorm + adaLN modulate, BF16 -> BF16
+    nbytes = 2 * n * d * 2
+    sets = _sets(nbytes)
+    xs = [randn(1, n, d) for _ in range(sets)]
+    outs = [torch.empty(1, n, d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    w = 1 + randn(d, scale=0.02, dtype=torch.float32)
+    mods = randn(1, 1, 6 * d, scale=0.1, dtype=torch.float32)
+    ms = _time(lambda i: K.rms_norm_modulate(xs[i % sets], w, mods[..., :d], mods[..., d:2 * d], eps,
+                                             torch.bfloat16, out=outs[i % sets]), iters)
+    results.append({"kernel": "rms_norm_modulate", "shape": [1, n, d], "bytes": nbytes, "sets": sets, "us": ms * 1e3})
+    del xs, outs
+
+    # qk-RMSNorm + RoPE of Q (20 heads) and K (5 heads)
+    img = tables.rope_2d_angles(128, 64, 64, 10000.0, 16.0, "isotropic")
+    txt = tables.rope_1d_angles(128, 256, 10000.0)
+    cos, sin = tables.cos_sin(txt, img, device=dev)
+    nbytes = 2 * (n * heads * 128 * 2) + 2 * (n * kv_heads * 128 * 2) + 2 * cos.numel() * 4
+    sets = _sets(nbytes)
+    qs = [randn(1, n, heads * 128) for _ in range(sets)]
+    ks = [randn(1, n, kv_heads * 128) for _ in range(sets)]
+    qo = [torch.empty(1, heads, n, 128, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    ko = [torch.empty(1, kv_heads, n, 128, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    qw, kw = 1 + randn(128, scale=0.02, dtype=torch.float32), 1 + randn(128, scale=0.02, dtype=torch.float32)
+
+    def qk(i):
+        j = i % sets
+        K.qk_norm_rope(qs[j], qw, cos, sin, eps, heads, out=qo[j])
+        K.qk_norm_rope(ks[j], kw, cos, sin, eps, kv_heads, out=ko[j])
+
+    ms = _time(qk, iters)
+    results.append({"kernel": "qk_norm_rope (Q + K)", "shape": [1, n, (heads + kv_heads) * 128], "bytes": nbytes,
+                    "sets": sets, "us": ms * 1e3})
+    del qs, ks, qo, ko
+
+    # post-norm gated residual, FP32 residual in place, BF16 branch
+    nbytes = 2 * n * d * 4 + n * d * 2
+    sets = _sets(nbytes)
+    res = [randn(1, n, d, dtype=torch.float32) for _ in range(sets)]
+    br = [randn(1, n, d) for _ in range(sets)]
+    ms = _time(lambda i: K.gated_residual_rms_norm_(res[i % sets], br[i % sets], w, mods[..., 2 * d:3 * d], eps), iters)
+    results.append({"kernel": "gated_residual_rms_norm_", "shape": [1, n, d], "bytes": nbytes, "sets": sets,
+                    "us": ms * 1e3})
+    outs = [torch.empty(1, n, d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    ms = _time(lambda i: K.gated_residual_norm_modulate_(res[i % sets], br[i % sets], w, mods[..., 2 * d:3 * d], eps,
+                                                         w, mods[..., 3 * d:4 * d], mods[..., 4 * d:5 * d],
+                                                         outs[i % sets]), iters)
+    results.append({"kernel": "gated_residual_norm_modulate_ (fused pair)", "shape": [1, n, d],
+                    "bytes": nbytes + n * d * 2, "sets": sets, "us": ms * 1e3})
+    del res, br, outs
+
+    # reference point: a plain device copy of the same size class (44.6 MB in, 44.6 MB out)
+    nbytes = 2 * n * d * 4
+    sets = _sets(nbytes)
+    src = [randn(n * d, dtype=torch.float32) for _ in range(sets)]
+    dst = [torch.empty(n * d, device=dev) for _ in range(sets)]
+    ms = _time(lambda i: dst[i % sets].copy_(src[i % sets]), iters)
+    results.append({"kernel": "copy (torch, reference)", "shape": [n * d], "bytes": nbytes, "sets": sets,
+                    "us": ms * 1e3})
+    for r in results:
+        r["GB/s"] = r["bytes"] / (r["us"] * 1e-6) / 1e9
+        r["hbm_frac"] = r["GB/s"] / HBM_GBS
+    return results
+
+
+def gemm(m: int, n: int, k: int, tile: int = -1, iters: int = 20) -> dict:
+    a = torch.randn(m, k, device="cuda").to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, device="cuda")).to(torch.bfloat16)
+    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    _lib.call("iris_gemm_force_tile", tile)
+    try:
+        ms = _time(lambda i: K.linear(a, w, out=out), iters)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"kernel": "gemm_bf16", "m": m, "n": n, "k": k, "tile": tile, "us": ms * 1e3, "TFLOP/s": tflops,
+            "mfma_frac": tflops / MFMA_TFLOPS}
+
+
+def attention(b: int, h: int, hkv: int, n: int, iters: int = 20) -> dict:
+    n_pad = (n + 63) // 64 * 64
+    q = torch.randn(b, h, n_pad, 128, device="cuda").to(torch.bfloat16)
+    k = torch.randn(b, hkv, n_pad, 128, device="cuda").to(torch.bfloat16)
+    vt = torch.randn(b, hkv, 128, n_pad, device="cuda").to(torch.bfloat16)
+    out = torch.empty(b * n, h * 128, device="cuda", dtype=torch.bfloat16)
+    ms = _time(lambda i: K.flash_attention(q, k, vt, n, None, out, 0), iters)
+    tflops = 4.0 * b * n * n * h * 128 / (ms * 1e-3) / 1e12
+    return {"kernel": "flash_attn", "b": b, "heads": h, "kv_heads": hkv, "n": n, "us": ms * 1e3, "TFLOP/s": tflops,
+            "mfma_frac": tflops / MFMA_TFLOPS}
+
+
+def copy(gib: float, iters: int = 5) -> dict:
+    src = torch.ones(int(gib * (1 << 28)), device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    ms = _time(lambda i: dst.copy_(src), iters)
+    nbytes = 2 * src.numel() * 4
+    return {"kernel": "copy", "bytes": nbytes, "us": ms * 1e3, "GB/s": nbytes / (ms * 1e-3) / 1e9}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    sub.add_parser("fused-ops")
+    p = sub.add_parser("gemm")
+    p.add_argument("m", type=int)
+    p.add_argument("n", type=int)
+    p.add_argument("k", type=int)
+    p.add_argument("--tile", type=int, default=-1)
+    p = sub.add_parser("attention")
+    for name in ("b", "h", "hkv", "n"):
+        p.add_argument(name, type=int)
+    p = sub.add_parser("copy")
+    p.add_argument("gib", type=float, nargs="?", default=1.0)
+    args = ap.parse_args()
+    _lib.load()
+    if args.cmd == "fused-ops":
+        out = fused_ops()
+    elif args.cmd == "gemm":
+        out = gemm(args.m, args.n, args.k, args.tile)
+    elif args.cmd == "attention":
+        out = attention(args.b, args.h, args.hkv, args.n)
+    else:
+        out = copy(args.gib)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

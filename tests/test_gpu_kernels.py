@@ -60,6 +60,25 @@ def test_gated_residual_rms_norm(branch_dtype):
     torch.testing.assert_close(r.cpu(), want, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("shape", [(1, 4352, 2560), (2, 37, 256)])
+def test_gated_residual_fused_with_next_norm_modulate(shape):
+    b, n, d = shape
+    g = gen(22)
+    res = torch.randn(b, n, d, generator=g)
+    branch = torch.randn(b, n, d, generator=g).to(torch.bfloat16)
+    w, w2 = 1 + 0.02 * torch.randn(d, generator=g), 1 + 0.02 * torch.randn(d, generator=g)
+    mods = 0.1 * torch.randn(b, 1, 6 * d, generator=g)
+    gate, shift, scale = mods[..., :d], mods[..., d:2 * d], mods[..., 2 * d:3 * d]
+    new_res = res + gate * O.rms_norm(branch.float(), w, 1e-6)
+    want = O.modulate(O.rms_norm(new_res, w2, 1e-6), shift, scale)
+    r, md = res.to(DEV), mods.to(DEV)
+    out = torch.empty(b, n, d, device=DEV, dtype=torch.bfloat16)
+    K.gated_residual_norm_modulate_(r, branch.to(DEV), w.to(DEV), md[..., :d], 1e-6, w2.to(DEV), md[..., d:2 * d],
+                                    md[..., 2 * d:3 * d], out)
+    torch.testing.assert_close(r.cpu(), new_res, rtol=1e-5, atol=1e-5)
+    close_bf16(out, want)
+
+
 def _qk_reference(x, weight, cos, sin, heads, col_offset, eps=1e-6):
     b, n, _ = x.shape
     h = x[..., col_offset:col_offset + heads * 128].reshape(b, n, heads, 128).float()
