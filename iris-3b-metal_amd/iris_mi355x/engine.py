@@ -440,6 +440,10 @@ class HipIris:
                      (blk["fc1_w"], blk["fc1_b"]), (blk["fc2_w"], blk["fc2_b"]), next_norm, eps,
                      next_input=ws["hpix"])
 
+    def as_dit(self) -> "HipIrisDiT":
+        """The upstream ``IrisDiT`` call surface over this engine (the Turbo route)."""
+        return HipIrisDiT(self)
+
     # -- conditioning -------------------------------------------------------------------
     def encode_text(self, states: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
         """Encoder states ``[B, T, layers, dim]`` -> trunk text tokens (src/iris_metal/model.py:133-145).
@@ -448,3 +452,21 @@ class HipIris:
         step; it is not implemented on the GPU yet, so callers pass prepared tokens."""
         raise NotImplementedError("HipIris.encode_text: the text adapter is not on the HIP path yet; "
                                   "pass prepared text tokens [B, T, D] to __call__")
+
+
+class HipIrisDiT:
+    """``model(x, t, y, y_mask=, prepared_text=, precompute_modulation=).x`` over a ``HipIris``:
+    the upstream ``IrisDiT.forward`` surface the reference Turbo route calls
+    (src/iris_metal/pipeline.py:387-407, src/iris3b/models/dit.py:283-315)."""
+
+    def __init__(self, engine: HipIris):
+        self.engine = engine
+        self.cfg = engine.cfg
+
+    def __call__(self, x, t, y=None, y_mask=None, prepared_text=None, precompute_modulation=True, capture=()):
+        if capture:
+            raise ValueError("HipIrisDiT does not return intermediate block features")
+        text = prepared_text if prepared_text is not None else self.engine.encode_text(y, y_mask)
+        from types import SimpleNamespace
+
+        return SimpleNamespace(x=self.engine(x, t.reshape(-1), text))

@@ -63,6 +63,19 @@ def test_released_turbo_matches_oracle_sampler(released):
     check(got, want, "released turbo")
 
 
+def test_upstream_dit_surface_matches_engine(released):
+    """``as_dit()`` answers the upstream ``IrisDiT`` call of the Turbo route with ``.x``."""
+    cfg, sd, engine = released
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 3, 32, 32, generator=g).to(DEV)
+    t = torch.tensor([938.0]).to(DEV)
+    text = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g).to(DEV)
+    out = engine.as_dit()(x, t, None, y_mask=None, prepared_text=text, precompute_modulation=True)
+    assert torch.equal(out.x, engine(x, t, text))
+    with pytest.raises(NotImplementedError):
+        engine.as_dit()(x, t, torch.zeros(1, 16, 3, 64, device=DEV), y_mask=torch.ones(1, 16, device=DEV))
+
+
 def test_unsupported_topology_is_rejected():
     from iris_mi355x.config import TINY
 
