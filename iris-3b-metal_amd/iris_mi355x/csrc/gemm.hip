@@ -203,6 +203,73 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
 
   // epilogue: acc[i][j][r] = C[m, n] with n = tile + 8 (r / 4) + 4 g + r % 4, m = tile + l32
   const long ldc = p.ldc;
+  if constexpr (sizeof(TC) == 2) {
+    // BF16 output: stage the tile through LDS (the K ring is free once every wave is past its
+    // last MFMA) so that each store instruction writes whole 512-byte row segments instead of
+    // 16-byte pieces of 32 rows. 4-element unit u of row r sits at unit u ^ 2 (r & MASK).
+    constexpr int OUT_N = EPI == IRIS_EPI_SILU_MUL ? BN / 2 : BN;
+    constexpr int UNITS = OUT_N / 4;
+    constexpr int MASK = (UNITS / 2 - 1) < 15 ? (UNITS / 2 - 1) : 15;
+    static_assert(BM * OUT_N <= STAGES * STAGE, "output tile must fit in the LDS ring");
+    bf16* cl = lds;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int r = wm * WM + j * 32 + l32;
+      bf16* crow_l = cl + r * OUT_N;
+      const int sw = 2 * (r & MASK);
+      if constexpr (EPI == IRIS_EPI_SILU_MUL) {
+#pragma unroll
+        for (int i = 0; i < FN; i += 2) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = silu(acc[i][j][4 * q + e]) * acc[i + 1][j][4 * q + e];
+            const int u = ((wn * WN + i * 32) / 2 + 8 * q + 4 * g) / 4;
+            store_out4(crow_l + 4 * (u ^ sw), v[0], v[1], v[2], v[3]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int nl = wn * WN + i * 32 + 8 * q + 4 * g;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
+            if (bias) {
+              const f32x4 bv = load4(bias + min(tn * BN + nl, N - 4));
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] += bv[e];
+            }
+            store_out4(crow_l + 4 * ((nl / 4) ^ sw), v[0], v[1], v[2], v[3]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int CHUNKS = OUT_N / 8;  // 16-byte chunks per row
+    const int n_out = EPI == IRIS_EPI_SILU_MUL ? N / 2 : N;
+    const int col0 = tn * OUT_N;
+#pragma unroll 4
+    for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
+      const int r = idx / CHUNKS;
+      const int c = idx - r * CHUNKS;
+      const int m = tm * BM + r;
+      const int n0 = col0 + 8 * c;
+      if (m >= M || n0 >= n_out) continue;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * OUT_N + 8 * (c ^ (r & MASK)));
+      TC* dst = C + static_cast<long>(m) * ldc + n0;
+      if (n0 + 8 <= n_out) {
+        *reinterpret_cast<bf16x8*>(dst) = v;
+      } else {
+        *reinterpret_cast<bf16x4*>(dst) = bf16x4{v[0], v[1], v[2], v[3]};  // n_out % 4 == 0
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int m = tm * BM + wm * WM + j * 32 + l32;
