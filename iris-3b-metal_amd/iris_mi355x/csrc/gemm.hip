@@ -209,7 +209,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
     // 16-byte pieces of 32 rows. 4-element unit u of row r sits at unit u ^ 2 (r & MASK).
     constexpr int OUT_N = EPI == IRIS_EPI_SILU_MUL ? BN / 2 : BN;
     constexpr int UNITS = OUT_N / 4;
-    constexpr int MASK = (UNITS / 2 - 1) < 15 ? (UNITS / 2 - 1) : 15;
+    // the XOR must stay inside the row: within 32-unit blocks when the row holds whole ones,
+    // else within 16-unit blocks (rows of 48 units for BN = 192)
+    constexpr int MASK = UNITS % 32 == 0 ? 15 : (UNITS % 16 == 0 ? 7 : 0);
+    static_assert(UNITS % 16 == 0 || UNITS < 16, "output tile width");
     static_assert(BM * OUT_N <= STAGES * STAGE, "output tile must fit in the LDS ring");
     bf16* cl = lds;
     __syncthreads();
@@ -315,10 +318,15 @@ int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   const dim3 grid(args.total_tiles);
   const dim3 block(64 * WGM * WGN);
   if (epilogue == IRIS_EPI_SILU_MUL) {
-    if (c_dtype == IRIS_BF16)
-      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, bf16><<<grid, block, 0, stream>>>(args);
-    else
-      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, float><<<grid, block, 0, stream>>>(args);
+    // the SwiGLU epilogue pairs 32-column blocks inside one wave: an even count per wave
+    if constexpr ((BN / WGN / 32) % 2 == 0) {
+      if (c_dtype == IRIS_BF16)
+        gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, bf16><<<grid, block, 0, stream>>>(args);
+      else
+        gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, float><<<grid, block, 0, stream>>>(args);
+    } else {
+      return fail(IRIS_E_UNSUPPORTED, "gemm: tile %dx%d has no SwiGLU epilogue", BM, BN);
+    }
   } else {
     if (c_dtype == IRIS_BF16)
       gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_NONE, bf16><<<grid, block, 0, stream>>>(args);
@@ -333,17 +341,37 @@ struct TileShape {
 };
 // 0: 256x256 BK64 x2 (4 waves), 1: 256x256 BK32 x4 (4 waves), 2: 256x256 BK64 x2 (8 waves),
 // 3: 128x128 BK64 x2 (4 waves, 2 workgroups per CU), 4: 256x256 BK32 x4 (8 waves),
-// 5: 256x128 BK64 x2 (4 waves)
-constexpr TileShape kTiles[] = {{256, 256, 64, 2}, {256, 256, 32, 4}, {256, 256, 64, 2},
-                                {128, 128, 64, 2}, {256, 256, 32, 4}, {256, 128, 64, 2}};
+// 5: 256x128 BK64 x2 (4 waves), 6: 256x256 BK64 x2 (16 waves), 7: 256x128 BK64 x3 (8 waves),
+// 8: 256x192 BK64 x2 (8 waves), 9: 192x256 BK64 x2 (8 waves)
+constexpr TileShape kTiles[] = {{256, 256, 64, 2}, {256, 256, 32, 4}, {256, 256, 64, 2}, {128, 128, 64, 2},
+                                {256, 256, 32, 4}, {256, 128, 64, 2}, {256, 256, 64, 2}, {256, 128, 64, 3},
+                                {256, 192, 64, 2}, {192, 256, 64, 2}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-// Tile shape (measured on the trunk and pixel-stage shapes): 256x256 with 8 waves once there
-// are enough tiles to cover the 256 CUs, else 128x128 (two workgroups per CU).
-int pick_tile(long m_total, int n, int forced) {
+// Tile shape: the candidate with the least estimated time, rounds of workgroups over the
+// 256 CUs (the last round costs as much as a full one) x tile area / relative per-CU rate.
+// Rates were measured on the trunk and pixel-stage shapes: 256x256 / 8 waves 1.0, 256x192
+// and 192x256 0.97, 128x128 at two workgroups per CU 0.9. The SwiGLU epilogue excludes the
+// 192-column tile.
+int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
   if (forced >= 0) return forced;
-  const long t256 = ((m_total + 255) / 256) * ((n + 255) / 256);
-  return t256 >= 160 ? 2 : 3;
+  struct Candidate {
+    int tile, per_cu;
+    double rate;
+  };
+  const Candidate candidates[] = {{2, 1, 1.0}, {8, 1, 0.97}, {9, 1, 0.97}, {3, 2, 0.9}};
+  int best = 2;
+  double best_cost = 0.0;
+  for (const Candidate& c : candidates) {
+    if (c.tile == 8 && epilogue == IRIS_EPI_SILU_MUL) continue;
+    const TileShape t = kTiles[c.tile];
+    long tiles = 0;
+    for (int i = 0; i < groups; ++i) tiles += static_cast<long>((m[i] + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+    const long slots = 256L * c.per_cu;
+    const double cost = static_cast<double>((tiles + slots - 1) / slots) * t.bm * t.bn * c.per_cu / c.rate;
+    if (best_cost == 0.0 || cost < best_cost) best = c.tile, best_cost = cost;
+  }
+  return best;
 }
 
 int g_forced_tile = -1;
@@ -383,7 +411,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 31), "gemm: weight too large for 32-bit offsets");
   for (int i = 0; i < groups; ++i)
     IRIS_REQUIRE(static_cast<long>(m[i]) * lda < (1L << 31), "gemm: activation too large for 32-bit offsets");
-  const int tile = pick_tile(m_total, n, g_forced_tile);
+  const int tile = pick_tile(m, groups, n, epilogue, g_forced_tile);
   const TileShape shape = kTiles[tile];
   const int bm = shape.bm;
   const int bn = shape.bn;
@@ -415,8 +443,17 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
       return launch_tile<128, 128, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
     case 4:
       return launch_tile<256, 256, 32, 4, 2, 4>(args, c_dtype, epilogue, stream);
-    default:
+    case 5:
       return launch_tile<256, 128, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
+    case 6:
+      return launch_tile<256, 256, 64, 2, 4, 4>(args, c_dtype, epilogue, stream);
+    case 7:
+      return launch_tile<256, 128, 64, 3, 4, 2>(args, c_dtype, epilogue, stream);
+    case 8:
+      IRIS_REQUIRE(epilogue == IRIS_EPI_NONE, "gemm: the 192-wide tile has no SwiGLU epilogue");
+      return launch_tile<256, 192, 64, 2, 4, 2>(args, c_dtype, epilogue, stream);
+    default:
+      return launch_tile<192, 256, 64, 2, 2, 4>(args, c_dtype, epilogue, stream);
   }
 }
 
