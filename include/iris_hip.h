@@ -93,7 +93,8 @@ int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int
                     long gate_batch_rows0, long gate_batch_rows1, hipStream_t stream);
 
 /* Tuning hook for the benchmark sweep: force the attention variant (0: 64 query rows per wave,
- * 2 K/V stages; 1: 64 rows, 3 stages; 2: 32 rows, 2 stages) or restore the automatic choice (-1).
+ * 2 stages of 64 keys; 1: 64 rows, 3 x 64 keys; 2: 32 rows, 2 x 64 keys; 3: 32 rows, 4 x 32 keys;
+ * 4: 32 rows, 3 x 32 keys) or restore the automatic choice (-1).
  * No counterpart in the reference. */
 int iris_flash_attn_force_variant(int variant);
 

@@ -3,30 +3,30 @@
 //
 // Workgroup = 4 waves sharing one K/V head: with G = heads / kv_heads query heads per K/V
 // head, a workgroup serves hpw = min(G, 4) of them and 32 * QB * 4 / hpw query rows, one
-// wave per (query head, 32*QB-row block). K/V tiles of 64 keys go global -> LDS with
+// wave per (query head, 32*QB-row block). K/V tiles of KVT keys go global -> LDS with
 // global_load_lds_dwordx4 (no register staging) into a ring of STAGES buffers, and are
 // read by all four waves.
 //
 // Each wave computes S^T = K Q^T (v_mfma_f32_32x32x16_bf16, K fragments from LDS, Q
-// fragments held in registers), so every lane owns one query column and 32 of the 64 keys
+// fragments held in registers), so every lane owns one query column and half of the keys
 // of the tile: the online-softmax row max / sum need a single cross-lane exchange (lane ^ 32).
 // The probabilities, converted to bf16 in place, are exactly the B operand of O^T = V^T P^T
 // (with a fixed permutation of the keys inside each 16-key step, applied identically to the
 // V^T fragments), so P never leaves registers. V arrives transposed ([d, token]) with the
 // middle two 4-key quads of every 16 keys swapped, so each V^T fragment is one 16-byte read.
 //
-// LDS: K rows are 256 bytes, chunk c of key row r at chunk c ^ (r % 16); V^T rows are 128
-// bytes, chunk c of row d at c ^ ((d / 2) % 8): the 16-lane phases of ds_read_b128 hit
-// 64 distinct banks.
+// The softmax is VALU work beside the MFMAs, so it is kept short: exponentials are the bare
+// v_exp_f32 (results below 2^-126 flush to zero, far under bf16 resolution of P), and the
+// running output is rescaled only when the running max of some query column moved.
+//
+// LDS: K rows are 256 bytes, V^T rows 2*KVT bytes; chunk c of row r is stored at chunk
+// c ^ swz(r) so the 16-lane phases of ds_read_b128 hit 64 distinct banks.
 #include "iris_common.hpp"
 
 namespace iris {
 namespace {
 
 constexpr int kHd = 128;
-constexpr int kKv = 64;                  // keys per tile
-constexpr int kTile = kKv * kHd;         // elements of one K (or V^T) tile
-constexpr int kLoadsPerWave = 4;         // 1 KB loads per wave per operand per tile
 
 struct AttnArgs {
   const bf16* q;
@@ -50,10 +50,25 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int QB, int STAGES>
-__global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
-  constexpr int STAGE = 2 * kTile;  // K tile then V^T tile
-  constexpr int LPW = 2 * kLoadsPerWave;
+// Chunk swizzle for LDS rows of CPR 16-byte chunks: rows of 256 bytes use c ^ (r % 16), of
+// 128 bytes c ^ ((r / 2) % 8), of 64 bytes c ^ ((r / 4) % 4); 16 consecutive rows read at
+// one logical chunk then cover all 64 banks.
+template <int CPR>
+__device__ __forceinline__ int swz(int r) {
+  return (r / (16 / CPR)) % CPR;
+}
+
+template <int QB, int STAGES, int KVT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2 : 1))) void flash_attn_kernel(
+    AttnArgs p) {  // 32-row waves: two workgroups per CU (<= 256 registers per lane)
+  constexpr int KB = KVT / 32;     // 32-key blocks per tile
+  constexpr int TILE = KVT * kHd;  // elements of one K (or V^T) tile
+  constexpr int STAGE = 2 * TILE;  // K tile then V^T tile
+  constexpr int LOADS = KVT / 16;  // 1 KB loads per wave per operand per tile
+  constexpr int LPW = 2 * LOADS;
+  constexpr int VCPR = KVT / 8;    // 16-byte chunks per V^T row
+  constexpr int VRPL = 64 / VCPR;  // V^T rows per 1 KB load
+  static_assert(KVT == 32 || KVT == 64, "K/V tile of 32 or 64 keys");
   static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64, "pipeline depth");
   __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
@@ -89,27 +104,25 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
 
   const bf16* kh = p.k + (static_cast<long>(b) * p.kv_heads + kvh) * n_pad * kHd;
   const bf16* vh = p.vt + (static_cast<long>(b) * p.kv_heads + kvh) * kHd * n_pad;
-  // per-lane fetch offsets: K load j of wave w covers key rows 4 (4 w + j) .. +4 (16 chunks each),
-  // V^T load j covers dim rows 8 (4 w + j) .. +8 (8 chunks each)
-  int k_off[kLoadsPerWave], v_off[kLoadsPerWave];
+  // per-lane fetch offsets: K load j of wave w covers key rows 4 (LOADS w + j) .. +4 (16 chunks
+  // each), V^T load j covers dim rows VRPL (LOADS w + j) .. +VRPL (VCPR chunks each)
+  int k_off[LOADS], v_off[LOADS];
 #pragma unroll
-  for (int j = 0; j < kLoadsPerWave; ++j) {
-    const int kr = (w * kLoadsPerWave + j) * 4 + (lane >> 4);
-    k_off[j] = kr * kHd + 8 * ((lane & 15) ^ (kr & 15));
-    const int vd = (w * kLoadsPerWave + j) * 8 + (lane >> 3);
-    v_off[j] = vd * static_cast<int>(n_pad) + 8 * ((lane & 7) ^ ((vd >> 1) & 7));
+  for (int j = 0; j < LOADS; ++j) {
+    const int kr = (w * LOADS + j) * 4 + (lane >> 4);
+    k_off[j] = kr * kHd + 8 * ((lane & 15) ^ swz<16>(kr));
+    const int vd = (w * LOADS + j) * VRPL + lane / VCPR;
+    v_off[j] = vd * static_cast<int>(n_pad) + 8 * ((lane % VCPR) ^ swz<VCPR>(vd));
   }
   auto issue = [&](int t, int stage) {
     bf16* kl = lds + stage * STAGE;
-    bf16* vl = kl + kTile;
-    const bf16* kt = kh + static_cast<long>(t) * kKv * kHd;
-    const bf16* vt = vh + static_cast<long>(t) * kKv;
+    bf16* vl = kl + TILE;
+    const bf16* kt = kh + static_cast<long>(t) * KVT * kHd;
+    const bf16* vt = vh + static_cast<long>(t) * KVT;
 #pragma unroll
-    for (int j = 0; j < kLoadsPerWave; ++j) {
-      __builtin_amdgcn_global_load_lds((const void*)(kt + k_off[j]), (void*)(kl + (w * kLoadsPerWave + j) * 512), 16,
-                                       0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vt + v_off[j]), (void*)(vl + (w * kLoadsPerWave + j) * 512), 16,
-                                       0, 0);
+    for (int j = 0; j < LOADS; ++j) {
+      __builtin_amdgcn_global_load_lds((const void*)(kt + k_off[j]), (void*)(kl + (w * LOADS + j) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vt + v_off[j]), (void*)(vl + (w * LOADS + j) * 512), 16, 0, 0);
     }
   };
 
@@ -123,7 +136,7 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
   for (int qb = 0; qb < QB; ++qb) m_run[qb] = -INFINITY, l_run[qb] = 0.0f;
   const float sl2 = p.scale_log2;
 
-  const int n_tiles = (p.n + kKv - 1) / kKv;
+  const int n_tiles = (p.n + KVT - 1) / KVT;
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < n_tiles) issue(s, s);
@@ -135,33 +148,33 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
     __builtin_amdgcn_s_barrier();  // tile t visible; stage (t-1) % STAGES no longer read
     if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
     const bf16* kl = lds + (t % STAGES) * STAGE;
-    const bf16* vl = kl + kTile;
+    const bf16* vl = kl + TILE;
 
     // S^T[key, q] for keys kb*32 + (8 (r/4) + 4 g + r%4), queries qb*32 + l32
-    f32x16 s[2][QB];
+    f32x16 s[KB][QB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) s[kb][qb] = f32x16{};
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
-      bf16x8 kf[2];
+      bf16x8 kf[KB];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < KB; ++kb) {
         const int r = kb * 32 + l32;
-        kf[kb] = *reinterpret_cast<const bf16x8*>(kl + r * kHd + 8 * ((2 * st + g) ^ (r & 15)));
+        kf[kb] = *reinterpret_cast<const bf16x8*>(kl + r * kHd + 8 * ((2 * st + g) ^ swz<16>(r)));
       }
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
           s[kb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[qb][st], s[kb][qb], 0, 0, 0);
     }
 
-    const int kv0 = t * kKv;
-    if (kv0 + kKv > p.n) {  // tail tile: keys >= n do not exist
+    const int kv0 = t * KVT;
+    if (kv0 + KVT > p.n) {  // tail tile: keys >= n do not exist (every tile holds at least one key)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kv0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -176,31 +189,34 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
     for (int qb = 0; qb < QB; ++qb) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run[qb], mx * sl2);
-      const float alpha = exp2f(m_run[qb] - m_new);
-      m_run[qb] = m_new;
+      if (__any(m_new != m_run[qb])) {  // wave-uniform branch; alpha is 1 where the max held
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
+        m_run[qb] = m_new;
+      }
       float sum = 0.0f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float pv = exp2f(s[kb][qb][r] * sl2 - m_new);
+          const float pv = __builtin_amdgcn_exp2f(s[kb][qb][r] * sl2 - m_new);
           s[kb][qb][r] = pv;
           sum += pv;
         }
-      l_run[qb] = l_run[qb] * alpha + sum;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
+      l_run[qb] += sum;
     }
 
     // O^T[d, q] += V^T[d, keys] P^T[keys, q], 16 keys per MFMA step: k-index g*8 + m is
     // key kb*32 + 16 jj + 8 (m / 4) + 4 g + m % 4 for both operands.
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         bf16x8 pf[QB];
@@ -212,7 +228,7 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const int d = db * 32 + l32;
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vl + d * kKv + 8 * (c ^ ((d >> 1) & 7)));
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vl + d * KVT + 8 * (c ^ swz<VCPR>(d)));
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
             o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb], o[db][qb], 0, 0, 0);
@@ -255,6 +271,13 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs p) {
   }
 }
 
+struct Variant {
+  int qb, stages, kvt;
+};
+// 0: 64 query rows per wave, 2 stages of 64 keys; 1: 64 rows, 3 x 64 keys; 2: 32 rows,
+// 2 x 64 keys; 3: 32 rows, 4 x 32 keys; 4: 32 rows, 3 x 32 keys
+constexpr Variant kVariants[] = {{2, 2, 64}, {2, 3, 64}, {1, 2, 64}, {1, 4, 32}, {1, 3, 32}};
+constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 int g_attn_variant = -1;
 
 }  // namespace
@@ -300,30 +323,44 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   args.n = static_cast<int>(n);
   args.n_pad = static_cast<int>(n_pad);
   args.n_split = static_cast<int>(n_split);
-  // variant: 0 = 64 rows per wave, 2 stages; 1 = 64 rows, 3 stages; 2 = 32 rows, 2 stages
   args.hpw = group < 4 ? group : 4;
-  const long wg64 = static_cast<long>(batch) * kv_heads * (group / args.hpw) * ((n + 64 * 4 / args.hpw - 1) / (64 * 4 / args.hpw));
-  const int variant = g_attn_variant >= 0 ? g_attn_variant : (wg64 >= 512 ? 1 : 2);
-  const int qb = variant == 2 ? 1 : 2;
-  args.rows_per_wg = 32 * qb * 4 / args.hpw;
+  // 32-row waves at two workgroups per CU measured fastest at every Iris shape (trunk 4352 and
+  // 1280 tokens, pixel 4096): the softmax of one workgroup overlaps the MFMAs of the other.
+  const int variant = g_attn_variant >= 0 ? g_attn_variant : 2;
+  const Variant v = kVariants[variant];
+  args.rows_per_wg = 32 * v.qb * 4 / args.hpw;
   args.n_qblocks = static_cast<int>((n + args.rows_per_wg - 1) / args.rows_per_wg);
   args.n_hgroups = group / args.hpw;
   const long total = static_cast<long>(batch) * kv_heads * args.n_hgroups * args.n_qblocks;
   IRIS_REQUIRE(total < (1L << 31), "flash_attn: grid too large");
   args.total_wg = static_cast<int>(total);
   args.scale_log2 = scale * 1.4426950408889634f;
-  if (variant == 0)
-    flash_attn_kernel<2, 2><<<dim3(args.total_wg), 256, 0, stream>>>(args);
-  else if (variant == 1)
-    flash_attn_kernel<2, 3><<<dim3(args.total_wg), 256, 0, stream>>>(args);
-  else
-    flash_attn_kernel<1, 2><<<dim3(args.total_wg), 256, 0, stream>>>(args);
+  const dim3 grid(args.total_wg);
+  switch (variant) {
+    case 0:
+      flash_attn_kernel<2, 2, 64><<<grid, 256, 0, stream>>>(args);
+      break;
+    case 1:
+      flash_attn_kernel<2, 3, 64><<<grid, 256, 0, stream>>>(args);
+      break;
+    case 2:
+      flash_attn_kernel<1, 2, 64><<<grid, 256, 0, stream>>>(args);
+      break;
+    case 3:
+      flash_attn_kernel<1, 4, 32><<<grid, 256, 0, stream>>>(args);
+      break;
+    default:
+      flash_attn_kernel<1, 3, 32><<<grid, 256, 0, stream>>>(args);
+      break;
+  }
   return check_launch("flash_attn");
 }
 
-// Tuning hook: force an attention variant (0..2) or restore the automatic choice (-1).
+// Tuning hook: force an attention variant (an index into kVariants) or restore the automatic
+// choice (-1).
 extern "C" int iris_flash_attn_force_variant(int variant) {
-  IRIS_REQUIRE(variant >= -1 && variant <= 2, "flash_attn_force_variant: variant in -1..2");
+  IRIS_REQUIRE(variant >= -1 && variant < kNumVariants, "flash_attn_force_variant: variant in -1..%d",
+               kNumVariants - 1);
   g_attn_variant = variant;
   return IRIS_OK;
 }

@@ -212,9 +212,10 @@ def _attn_inputs(b, h, hkv, n, seed):
     return q, k, v, qd.to(DEV), kd.to(DEV), vt.to(DEV)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2])
-def test_flash_attention_variants(variant):
-    b, h, hkv, n = 1, 8, 2, 333
+@pytest.mark.parametrize("n", [333, 352])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+def test_flash_attention_variants(variant, n):
+    b, h, hkv = 1, 8, 2
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 16)
     want = O.attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(b, n, h * 128)
     out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
