@@ -248,6 +248,7 @@ def main() -> None:
 
     turbo_s = None
     if not args.no_turbo:
+        turbo_sample(engine, noise, text)  # first call allocates the sampler's buffers
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         turbo_sample(engine, noise, text)

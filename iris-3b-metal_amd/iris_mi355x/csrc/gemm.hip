@@ -68,7 +68,23 @@ __device__ __forceinline__ int swz(int r) {
   return (r / (16 / CPR)) % CPR;
 }
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int EPI, typename TC>
+// Loads of part `part` when a K tile's lpw loads are dealt round-robin into `parts` parts.
+constexpr int part_loads(int lpw, int parts, int part) { return part < parts ? (lpw - part + parts - 1) / parts : 0; }
+
+// Instruction order inside one k-step: one MFMA (its operands were read a whole k-step
+// earlier), then every fragment read of the next k-step (NR), then this k-step's global loads,
+// then the remaining MFMAs (NM in all), so each read has all but one MFMA of the k-step to
+// land. Without these hints the scheduler sinks the reads below the MFMAs that free their
+// registers and waits for them at the start of the next k-step with nothing left in flight.
+template <int NR, int NM, int LOADS>
+__device__ __forceinline__ void order_kstep() {
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // MFMA
+  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);                           // DS read
+  if constexpr (LOADS > 0) __builtin_amdgcn_sched_group_barrier(0x010, LOADS, 0);  // VMEM
+  __builtin_amdgcn_sched_group_barrier(0x008, NM - 1, 0);                       // MFMA
+}
+
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int PARTS, int EPI, typename TC>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
   constexpr int NW = WGM * WGN;             // waves per workgroup
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -82,6 +98,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
   constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
   static_assert(A_LOADS * RPL * NW == BM && B_LOADS * RPL * NW == BN, "tile / wave split");
   static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64, "pipeline depth");
+  static_assert(PARTS >= 1 && PARTS <= 4 && PARTS <= KS && PARTS <= LPW, "load parts");
   __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
   int tile = xcd_remap(blockIdx.x, p.total_tiles);
@@ -125,19 +142,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
     const int r = (w * B_LOADS + i) * RPL + ld_r;
     b_off[i] = min(tn * BN + r, N - 1) * static_cast<int>(p.ldb) + 8 * (ld_p ^ swz<BK>(r));
   }
-  auto issue = [&](int kt, int stage) {
+  // The LPW loads of one K tile form PARTS parts (load j belongs to part j % PARTS, A loads
+  // numbered before B loads) so that they can be spread over several k-steps.
+  auto issue = [&](int kt, int stage, int part) {  // part < 0: all loads
     bf16* sa = lds + stage * STAGE;
     bf16* sb = sa + A_STAGE;
     // (explicit void* casts: without them the host pass silently drops the kernel stub)
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(A + a_off[i] + kt * BK),
-                                       (void*)(sa + (w * A_LOADS + i) * RPL * BK), 16, 0, 0);
+      if (part < 0 || i % PARTS == part)
+        __builtin_amdgcn_global_load_lds((const void*)(A + a_off[i] + kt * BK),
+                                         (void*)(sa + (w * A_LOADS + i) * RPL * BK), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(B + b_off[i] + kt * BK),
-                                       (void*)(sb + (w * B_LOADS + i) * RPL * BK), 16, 0, 0);
+      if (part < 0 || (A_LOADS + i) % PARTS == part)
+        __builtin_amdgcn_global_load_lds((const void*)(B + b_off[i] + kt * BK),
+                                         (void*)(sb + (w * B_LOADS + i) * RPL * BK), 16, 0, 0);
   };
+
 
   // fragment reads: row r, logical chunk 2 ks + g, stored at chunk (2 ks + g) ^ swz(r)
   int a_row[FM], b_row[FN];
@@ -167,39 +189,76 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
   // Software pipeline: the fragments of the next k-step are read from LDS while the MFMAs
   // of the current one run; the wait + barrier for K tile kt+1 sits before the last k-step
   // of tile kt, whose fragments are already in registers, so the stage being retired can be
-  // refilled right after that barrier.
+  // refilled right after that barrier. The refill of tile kt+STAGES starts there (part 0)
+  // and continues over the first PARTS-1 k-steps of tile kt+1 (parts 1..), so that the
+  // eight waves do not queue all their loads at the same moment.
   const int KT = p.k / BK;
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < KT) issue(s, s);
+    if (s < KT) issue(s, s, -1);
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
-  if (STAGES - 1 < KT) issue(STAGES - 1, STAGES - 1);
+  issue(min(STAGES - 1, KT - 1), STAGES - 1, 0);
   read_frags(0, 0, 0);
-  for (int kt = 0; kt < KT; ++kt) {
+
+  auto mfmas = [&](int cur) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cur][i], xf[cur][j], acc[i][j], 0, 0, 0);
+  };
+  constexpr int NR = FN + FM, NM = FN * FM;
+  constexpr int L0 = part_loads(LPW, PARTS, 0), L1 = part_loads(LPW, PARTS, 1);
+  constexpr int L2 = part_loads(LPW, PARTS, 2), L3 = part_loads(LPW, PARTS, 3);
+
+  // Every K tile but the last: branch-free, so each k-step is one scheduling region. Refills
+  // always issue; past the end they reload the final K tile into a retired stage that no
+  // pending tile occupies and nothing reads again (the loads are drained before the
+  // epilogue reuses the ring). Loads issued after tile kt+1's last part number
+  // (STAGES - 2) * LPW at the wait of tile kt, for every PARTS.
+  for (int kt = 0; kt + 1 < KT; ++kt) {
     const int stage = kt % STAGES;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int cur = ks & 1;
       if (ks + 1 < KS) {
         read_frags(stage, ks + 1, cur ^ 1);
-      } else if (kt + 1 < KT) {
-        // this wave's fragment reads of stage kt must have landed before the stage is refilled
-        if (kt + STAGES - 1 < KT)
-          wait_vmcnt_lgkm0<(STAGES - 2) * LPW>();
+        if (ks + 1 < PARTS) issue(min(kt + STAGES - 1, KT - 1), (kt + STAGES - 1) % STAGES, ks + 1);
+        mfmas(cur);
+        if (ks + 1 >= PARTS)
+          order_kstep<NR, NM, 0>();
+        else if (ks == 0)
+          order_kstep<NR, NM, L1>();
+        else if (ks == 1)
+          order_kstep<NR, NM, L2>();
         else
-          wait_vmcnt_lgkm0<0>();
+          order_kstep<NR, NM, L3>();
+      } else {
+        // tile kt+1 has landed (loads issued after it may still fly) and this wave's
+        // fragment reads of stage kt are done before the barrier lets the stage be refilled;
+        // the wait stays behind the previous k-step's MFMAs, which cover it
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt_lgkm0<(STAGES - 2) * LPW>();
         __builtin_amdgcn_s_barrier();
-        if (kt + STAGES < KT) issue(kt + STAGES, stage);
         read_frags((kt + 1) % STAGES, 0, cur ^ 1);
+        issue(min(kt + STAGES, KT - 1), stage, 0);
+        mfmas(cur);
+        order_kstep<NR, NM, L0>();
       }
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cur][i], xf[cur][j], acc[i][j], 0, 0, 0);
     }
   }
+  {  // last K tile
+    const int stage = (KT - 1) % STAGES;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KS) read_frags(stage, ks + 1, cur ^ 1);
+      mfmas(cur);
+      if (ks + 1 < KS) order_kstep<NR, NM, 0>();
+    }
+  }
+  wait_vmcnt<0>();
 
   // epilogue: acc[i][j][r] = C[m, n] with n = tile + 8 (r / 4) + 4 g + r % 4, m = tile + l32
   const long ldc = p.ldc;
@@ -313,7 +372,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
   }
 }
 
-template <int BM, int BN, int BK, int STAGES, int WGM, int WGN>
+template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int PARTS>
 int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   const dim3 grid(args.total_tiles);
   const dim3 block(64 * WGM * WGN);
@@ -321,50 +380,65 @@ int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
     // the SwiGLU epilogue pairs 32-column blocks inside one wave: an even count per wave
     if constexpr ((BN / WGN / 32) % 2 == 0) {
       if (c_dtype == IRIS_BF16)
-        gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, bf16><<<grid, block, 0, stream>>>(args);
+        gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, PARTS, IRIS_EPI_SILU_MUL, bf16><<<grid, block, 0, stream>>>(args);
       else
-        gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_SILU_MUL, float><<<grid, block, 0, stream>>>(args);
+        gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, PARTS, IRIS_EPI_SILU_MUL, float><<<grid, block, 0, stream>>>(args);
     } else {
       return fail(IRIS_E_UNSUPPORTED, "gemm: tile %dx%d has no SwiGLU epilogue", BM, BN);
     }
   } else {
     if (c_dtype == IRIS_BF16)
-      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_NONE, bf16><<<grid, block, 0, stream>>>(args);
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, PARTS, IRIS_EPI_NONE, bf16><<<grid, block, 0, stream>>>(args);
     else
-      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, IRIS_EPI_NONE, float><<<grid, block, 0, stream>>>(args);
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, PARTS, IRIS_EPI_NONE, float><<<grid, block, 0, stream>>>(args);
   }
   return check_launch("gemm_bf16");
 }
 
 struct TileShape {
-  int bm, bn, bk, stages;
+  int bm, bn, bk, stages, wgm, wgn, parts;
+  bool swiglu() const { return (bn / wgn / 32) % 2 == 0; }
 };
-// 0: 256x256 BK64 x2 (4 waves), 1: 256x256 BK32 x4 (4 waves), 2: 256x256 BK64 x2 (8 waves),
-// 3: 128x128 BK64 x2 (4 waves, 2 workgroups per CU), 4: 256x256 BK32 x4 (8 waves),
-// 5: 256x128 BK64 x2 (4 waves), 6: 256x256 BK64 x2 (16 waves), 7: 256x128 BK64 x3 (8 waves),
-// 8: 256x192 BK64 x2 (8 waves), 9: 192x256 BK64 x2 (8 waves)
-constexpr TileShape kTiles[] = {{256, 256, 64, 2}, {256, 256, 32, 4}, {256, 256, 64, 2}, {128, 128, 64, 2},
-                                {256, 256, 32, 4}, {256, 128, 64, 2}, {256, 256, 64, 2}, {256, 128, 64, 3},
-                                {256, 192, 64, 2}, {192, 256, 64, 2}};
+// BM x BN output tile, BK-deep K tiles in a ring of `stages`, wgm x wgn waves, the refill of a
+// K tile spread over `parts` k-steps.
+constexpr TileShape kTiles[] = {
+    {256, 256, 64, 2, 2, 4, 1},  // 0
+    {256, 256, 64, 2, 2, 4, 2},  // 1
+    {256, 192, 64, 2, 4, 2, 1},  // 2
+    {256, 192, 64, 2, 4, 2, 2},  // 3
+    {192, 256, 64, 2, 2, 4, 1},  // 4
+    {192, 256, 64, 2, 2, 4, 2},  // 5
+    {128, 128, 64, 2, 2, 2, 1},  // 6: two workgroups per CU
+    {256, 256, 32, 4, 2, 4, 1},  // 7
+    {256, 256, 32, 4, 2, 4, 2},  // 8
+    {256, 256, 64, 2, 2, 2, 1},  // 9: one wave per SIMD
+    {256, 256, 64, 2, 2, 2, 2},  // 10
+};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
+
+template <int I>
+int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
+  constexpr TileShape t = kTiles[I];
+  return launch_tile<t.bm, t.bn, t.bk, t.stages, t.wgm, t.wgn, t.parts>(args, c_dtype, epilogue, stream);
+}
 
 // Tile shape: the candidate with the least estimated time, rounds of workgroups over the
 // 256 CUs (the last round costs as much as a full one) x tile area / relative per-CU rate.
-// Rates were measured on the trunk and pixel-stage shapes: 256x256 / 8 waves 1.0, 256x192
-// and 192x256 0.97, 128x128 at two workgroups per CU 0.9. The SwiGLU epilogue excludes the
-// 192-column tile.
+// Rates were measured on the trunk and pixel-stage shapes (sustained runs, refills in two
+// parts): 256x256 / 8 waves 1.0, 192x256 0.98, 256x192 0.96, 128x128 at two workgroups per
+// CU 0.9. The SwiGLU epilogue excludes the 192-column tile.
 int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
   if (forced >= 0) return forced;
   struct Candidate {
     int tile, per_cu;
     double rate;
   };
-  const Candidate candidates[] = {{2, 1, 1.0}, {8, 1, 0.97}, {9, 1, 0.97}, {3, 2, 0.9}};
-  int best = 2;
+  const Candidate candidates[] = {{1, 1, 1.0}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
+  int best = 1;
   double best_cost = 0.0;
   for (const Candidate& c : candidates) {
-    if (c.tile == 8 && epilogue == IRIS_EPI_SILU_MUL) continue;
     const TileShape t = kTiles[c.tile];
+    if (epilogue == IRIS_EPI_SILU_MUL && !t.swiglu()) continue;
     long tiles = 0;
     for (int i = 0; i < groups; ++i) tiles += static_cast<long>((m[i] + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
     const long slots = 256L * c.per_cu;
@@ -432,28 +506,26 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   if (groups == 1) args.g1 = args.g0, args.g1.tile_begin = begin;
   args.total_tiles = begin;
   if (begin == 0) return IRIS_OK;
+  IRIS_REQUIRE(epilogue != IRIS_EPI_SILU_MUL || shape.swiglu(), "gemm: tile %dx%d has no SwiGLU epilogue", bm, bn);
+  static_assert(kNumTiles == 11, "one case per tile shape");
   switch (tile) {
-    case 0:
-      return launch_tile<256, 256, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
-    case 1:
-      return launch_tile<256, 256, 32, 4, 2, 2>(args, c_dtype, epilogue, stream);
-    case 2:
-      return launch_tile<256, 256, 64, 2, 2, 4>(args, c_dtype, epilogue, stream);
-    case 3:
-      return launch_tile<128, 128, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
-    case 4:
-      return launch_tile<256, 256, 32, 4, 2, 4>(args, c_dtype, epilogue, stream);
-    case 5:
-      return launch_tile<256, 128, 64, 2, 2, 2>(args, c_dtype, epilogue, stream);
-    case 6:
-      return launch_tile<256, 256, 64, 2, 4, 4>(args, c_dtype, epilogue, stream);
-    case 7:
-      return launch_tile<256, 128, 64, 3, 4, 2>(args, c_dtype, epilogue, stream);
-    case 8:
-      IRIS_REQUIRE(epilogue == IRIS_EPI_NONE, "gemm: the 192-wide tile has no SwiGLU epilogue");
-      return launch_tile<256, 192, 64, 2, 4, 2>(args, c_dtype, epilogue, stream);
+#define IRIS_TILE_CASE(I) \
+  case I:                 \
+    return launch_index<I>(args, c_dtype, epilogue, stream);
+    IRIS_TILE_CASE(0)
+    IRIS_TILE_CASE(1)
+    IRIS_TILE_CASE(2)
+    IRIS_TILE_CASE(3)
+    IRIS_TILE_CASE(4)
+    IRIS_TILE_CASE(5)
+    IRIS_TILE_CASE(6)
+    IRIS_TILE_CASE(7)
+    IRIS_TILE_CASE(8)
+    IRIS_TILE_CASE(9)
+    IRIS_TILE_CASE(10)
+#undef IRIS_TILE_CASE
     default:
-      return launch_tile<192, 256, 64, 2, 2, 4>(args, c_dtype, epilogue, stream);
+      return fail(IRIS_E_INVALID, "gemm: no tile shape %d", tile);
   }
 }
 

@@ -149,7 +149,7 @@ def _gemm_ref(a, w, bias=None):
     return out if bias is None else out + bias.cpu()
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2])
+@pytest.mark.parametrize("tile", list(range(-1, 11)))
 @pytest.mark.parametrize("mnk", [(300, 320, 128), (4096, 1280, 256), (1, 64, 64), (513, 260, 192)])
 def test_gemm_matches_fp32_reference(tile, mnk):
     m, n, k = mnk
@@ -180,7 +180,8 @@ def test_gemm_trunk_shapes(shape):
     torch.testing.assert_close(out[rows].cpu(), want, rtol=1e-4, atol=2e-4)
 
 
-def test_gemm_swiglu_epilogue_and_grouped_streams():
+@pytest.mark.parametrize("tile", [-1, 0, 1, 4, 5, 6, 7, 8, 9, 10])
+def test_gemm_swiglu_epilogue_and_grouped_streams(tile):
     d, hidden = 256, 682
     hp = 704
     g = gen(7)
@@ -188,7 +189,11 @@ def test_gemm_swiglu_epilogue_and_grouped_streams():
     packed = K.pack_swiglu(w1, w3, hp).to(torch.bfloat16)
     xs = [torch.randn(m, d, generator=g).to(torch.bfloat16) for m in (200, 33)]
     outs = [torch.full((m, hp), 7.0, device=DEV, dtype=torch.bfloat16) for m in (200, 33)]
-    K.linear_grouped([x.to(DEV) for x in xs], [packed.to(DEV)] * 2, None, outs, swiglu=True)
+    _lib.call("iris_gemm_force_tile", tile)
+    try:
+        K.linear_grouped([x.to(DEV) for x in xs], [packed.to(DEV)] * 2, None, outs, swiglu=True)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
     for x, o in zip(xs, outs):
         a = x.float() @ w1.to(torch.bfloat16).float().T
         b = x.float() @ w3.to(torch.bfloat16).float().T
