@@ -11,7 +11,10 @@ Prints one JSON line. Besides the driver's fields it carries:
   against the 2.5 PFLOP/s dense BF16 peak;
 - ``cpu_baseline``: the FP32 CPU oracle timed on this host on one dual, one single and one
   pixel block of the same 1024x1024 workload, composed into steps/s;
-- ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included).
+- ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included);
+- ``graph_ms_per_step``: the same step with the forward replayed from its recorded HIP graph.
+  The timed region itself launches eagerly, so that every GEMM launch can be bracketed by
+  events.
 """
 
 from __future__ import annotations
@@ -206,6 +209,7 @@ def main() -> None:
     print(f"[bench] drawing Iris-3B weights on {torch.cuda.get_device_name(dev)}", file=sys.stderr, flush=True)
     sd = synthetic_state_dict(cfg, seed=0, device=dev)
     engine = HipIris(cfg, sd, device=dev)
+    engine.graphs = False  # eager launches in the timed region (GEMM events); graphs timed after
     del sd
     torch.cuda.empty_cache()
 
@@ -246,6 +250,17 @@ def main() -> None:
     flops = step_flops(cfg, size, size, n_text)
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
 
+    # the same steps replayed from the recorded graph (recorded during the first two steps)
+    engine.graphs = True
+    for i in range(2):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    graph_ms = 1000.0 * (time.perf_counter() - t0) / args.steps
+
     turbo_s = None
     if not args.no_turbo:
         turbo_sample(engine, noise, text)  # first call allocates the sampler's buffers
@@ -283,6 +298,7 @@ def main() -> None:
                      "frac": gemm_tflops / BF16_PEAK_TFLOPS, "traffic": None,
                      "launches": gemm_launches, "avg_launch_us": 1000.0 * gemm_ms / max(gemm_launches, 1)},
         "turbo_4step_s": turbo_s,
+        "graph_ms_per_step": graph_ms,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))

@@ -84,21 +84,30 @@ class HipIris:
 
     ``HipIris(cfg, state_dict)`` or ``HipIris.from_module(dit)`` for an object exposing ``cfg``
     and ``state_dict()`` (an upstream ``IrisDiT``).
+
+    With ``graphs=True`` (the default) the inputs are copied into buffers the engine owns, the
+    forward over them is recorded once per input shape as a HIP graph (after one eager run,
+    whose result that call returns) and replayed by later calls: one launch instead of ~330,
+    whatever buffers the caller passes. The result is copied out of the engine's buffer.
     """
 
-    def __init__(self, cfg: ModelConfig, state_dict: dict[str, torch.Tensor], device: str | torch.device = "cuda"):
+    def __init__(self, cfg: ModelConfig, state_dict: dict[str, torch.Tensor], device: str | torch.device = "cuda",
+                 graphs: bool = True):
         cfg.validate()
         check_supported(cfg)
         self.cfg = cfg
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("HipIris runs on the GPU only")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.eps = cfg.norm_eps
         self.hidden_pad = _round_up(cfg.mlp_hidden, 64)
         self._prepare(state_dict)
         self._ws: dict | None = None
         self._ws_shape: _Shape | None = None
         self._tables: dict = {}
+        self.graphs = graphs
 
     @classmethod
     def from_module(cls, dit, device: str | torch.device = "cuda") -> "HipIris":
@@ -193,7 +202,7 @@ class HipIris:
     def _workspace(self, shape: _Shape) -> dict:
         if self._ws is not None and self._ws_shape == shape:
             return self._ws
-        self._ws = None
+        self._ws = None  # (with the buffers it points into goes the recorded graph)
         cfg, dev = self.cfg, self.device
         B, T = shape.batch, shape.n_text
         p = cfg.patch_size
@@ -265,13 +274,37 @@ class HipIris:
         if t.numel() != batch:
             raise ValueError(f"t must hold one model time per sample, got {tuple(t.shape)}")
         dev = self.device
-        x = x.to(dev, torch.float32).contiguous()
-        t = t.reshape(batch).to(dev, torch.float32).contiguous()
-        text = text.to(dev, torch.float32).contiguous()
-        ws = self._workspace(_Shape(batch, height, width, text.shape[1]))
+        shape = _Shape(batch, height, width, text.shape[1])
+        ws = self._workspace(shape)
         if out is None:
             out = torch.empty(batch, 3, height, width, device=dev, dtype=torch.float32)
-        self._forward(ws, x, t, text, out)
+        elif out.shape != x.shape or out.dtype != torch.float32 or not out.is_contiguous() or out.device != dev:
+            raise ValueError(f"out must be a contiguous FP32 {tuple(x.shape)} tensor on {dev}")
+        if not self.graphs:
+            x = x.to(dev, torch.float32).contiguous()
+            t = t.reshape(batch).to(dev, torch.float32).contiguous()
+            text = text.to(dev, torch.float32).contiguous()
+            self._forward(ws, x, t, text, out)
+            return out
+        if "graph" not in ws:
+            ws["x_in"] = torch.empty(batch, 3, height, width, device=dev, dtype=torch.float32)
+            ws["t_in"] = torch.empty(batch, device=dev, dtype=torch.float32)
+            ws["text_in"] = torch.empty(text.shape, device=dev, dtype=torch.float32)
+            ws["out_ws"] = torch.empty(batch, 3, height, width, device=dev, dtype=torch.float32)
+            ws["graph"] = None
+        args = (ws, ws["x_in"], ws["t_in"], ws["text_in"], ws["out_ws"])
+        ws["x_in"].copy_(x)
+        ws["t_in"].copy_(t.reshape(batch))
+        ws["text_in"].copy_(text)
+        if ws["graph"] is None:
+            self._forward(*args)  # this call's result, and every lazy set-up before recording
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._forward(*args)
+            ws["graph"] = graph
+        else:
+            ws["graph"].replay()
+        out.copy_(ws["out_ws"])
         return out
 
     def _forward(self, ws: dict, x: torch.Tensor, t: torch.Tensor, text: torch.Tensor, out: torch.Tensor) -> None:

@@ -26,7 +26,8 @@ def turbo_sample(model, noise: torch.Tensor, text: torch.Tensor, sigmas=TURBO_SI
                  num_train_timesteps: int = 1000, check=require_finite) -> torch.Tensor:
     """``model(x, t_model, text) -> v``; returns ``clean.clamp(-1, 1)`` after ``len(sigmas)`` steps."""
     dev = text.device
-    x = noise.to(dev, torch.float32).contiguous()
+    x = torch.empty(noise.shape, device=dev, dtype=torch.float32)
+    x.copy_(noise)  # the loop writes its two latent buffers; the caller's noise stays untouched
     batch = x.shape[0]
     # t = float32(sigma) * num_train_timesteps in FP32, as the reference's sigma tensor
     times = [torch.full((batch,), s, dtype=torch.float32) * num_train_timesteps for s in sigmas]
@@ -64,7 +65,8 @@ def dpm1_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor
                 num_timesteps: int = 1000) -> torch.Tensor:
     """First-order ``FlowDPMSolver.sample`` with CFG batching ``cat([uncond, cond])``."""
     grid = time_grid(steps, shift)
-    x = z.to(cond.device, torch.float32).contiguous()
+    x = torch.empty(z.shape, device=cond.device, dtype=torch.float32)
+    x.copy_(z)  # the loop writes its two latent buffers; the caller's z stays untouched
     batch = x.shape[0]
     x2 = torch.empty((2 * batch, *x.shape[1:]), device=x.device, dtype=torch.float32)
     text2 = torch.cat([uncond, cond]) if uncond is not None else None

@@ -59,8 +59,28 @@ def test_released_turbo_matches_oracle_sampler(released):
     noise = torch.randn(1, 3, 32, 32, generator=g)
     text = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g)
     want = O.turbo_sample(lambda x, t: O.forward(sd, cfg, x, t, prepared_text=text), noise)
-    got = turbo_sample(engine, noise.to(DEV), text.to(DEV))
+    noise_d = noise.to(DEV)
+    got = turbo_sample(engine, noise_d, text.to(DEV))
     check(got, want, "released turbo")
+    assert torch.equal(noise_d.cpu(), noise)  # the sampler keeps its own latent buffers
+
+
+def test_released_dpm1_cfg_matches_oracle_sampler(released):
+    """First-order FlowDPMSolver with classifier-free guidance (batch cat([uncond, cond])) and
+    a guidance interval that leaves the first step unguided."""
+    from iris_mi355x.sampling import dpm1_sample
+
+    cfg, sd, engine = released
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(1, 3, 32, 32, generator=g)
+    cond = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g)
+    uncond = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g)
+    kw = dict(steps=4, shift=4.0, cfg_scale=3.0, cfg_interval=(0.0, 0.95))
+    want = O.dpm_sample(lambda x, t, y: O.forward(sd, cfg, x, t, prepared_text=y), z, cond, uncond, order=1, **kw)
+    z_d = z.to(DEV)
+    got = dpm1_sample(engine, z_d, cond.to(DEV), uncond.to(DEV), **kw)
+    check(got, want, "released dpm1 cfg")
+    assert torch.equal(z_d.cpu(), z)
 
 
 def test_upstream_dit_surface_matches_engine(released):
@@ -106,3 +126,43 @@ def test_iris3b_shallow_forward_at_256px_matches_oracle(iris3b_blocks):
     engine = HipIris(cfg, sd, device=DEV)
     got = engine(x.to(DEV), t.to(DEV), text.to(DEV))
     check(got, want, "iris3b shallow 256px")
+
+
+def test_graph_replays_match_eager_forward(released):
+    """The recorded forward replays bit-identically to eager runs of the same kernels, across
+    several replays with eager work and synchronisation between them, for alternating caller
+    buffers, new input values, and after a shape change (which records a new graph)."""
+    cfg, sd, eager = released
+    eager.graphs = False
+    try:
+        graphed = HipIris(cfg, sd, device=DEV)
+        assert graphed.graphs
+        g = torch.Generator().manual_seed(11)
+        xs = [torch.randn(2, 3, 32, 48, generator=g).to(DEV) for _ in range(2)]
+        t = torch.tensor([300.0, 700.0]).to(DEV)
+        text = torch.randn(2, cfg.text_len, cfg.hidden_size, generator=g).to(DEV)
+        outs = [torch.empty_like(x) for x in xs]
+        recorded = None
+        for rep in range(4):
+            for x, out in zip(xs, outs):
+                graphed(x, t, text, out=out)
+                torch.cuda.synchronize()
+                want = eager(x, t, text)
+                assert torch.equal(out, want), f"replay {rep}"
+                if recorded is None:
+                    recorded = graphed._ws["graph"]
+                assert graphed._ws["graph"] is recorded  # one recording per shape
+            xs[0].mul_(0.9).add_(0.05)
+            t.add_(25.0)
+        # CPU inputs and a returned output work the same way
+        got = graphed(xs[1].cpu(), t.cpu(), text.cpu())
+        assert torch.equal(got, eager(xs[1], t, text))
+        # another shape records afresh
+        x3 = torch.randn(1, 3, 64, 40, generator=g).to(DEV)
+        t3 = torch.tensor([125.0]).to(DEV)
+        text3 = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g).to(DEV)
+        for _ in range(3):
+            assert torch.equal(graphed(x3, t3, text3), eager(x3, t3, text3))
+        assert graphed._ws["graph"] is not recorded
+    finally:
+        eager.graphs = True
