@@ -177,6 +177,15 @@ int iris_flow_euler(const float* x, const float* v, long n, float sigma, float s
 int iris_dpm1_update(const float* x, const float* v, long n, float s, float c_x, float c_x0, float* x_next,
                      hipStream_t stream);
 
+/* One step of the multistep FlowDPMSolver (src/iris3b/flow/solver.py:90-109, 130-139), FP32, in
+ * the reference's operation order: x0 = x - s*v, stored to x0_out when non-null (the next
+ * step's history); with x0_prev null the first-order step x_next = c_x*x - c_x0*x0, else the
+ * second-order one x_next = (c_x*x - c_x0*x0) - c_d*((x0 - x0_prev)/r0), where c_x = t/s0,
+ * c_x0 = (1-t)*expm1(-h), c_d = 0.5*(1-t)*expm1(-h) and r0 = h0/h. Outputs must not alias
+ * inputs. */
+int iris_dpm_update(const float* x, const float* v, const float* x0_prev, long n, float s, float c_x, float c_x0,
+                    float c_d, float r0, float* x_next, float* x0_out, hipStream_t stream);
+
 /* Classifier-free guidance combine (src/iris3b/flow/solver.py:72-74): out = u + scale*(c - u). */
 int iris_cfg_combine(const float* v_uncond, const float* v_cond, long n, float scale, float* out,
                      hipStream_t stream);

@@ -46,6 +46,7 @@ _SIGNATURES: dict[str, list] = {
     "iris_copy_rows": [P, P, c_int, c_long, c_int, c_long, c_long, c_long, c_long, P],
     "iris_flow_euler": [P, P, c_long, c_float, c_float, P, P, P],
     "iris_dpm1_update": [P, P, c_long, c_float, c_float, c_float, P, P],
+    "iris_dpm_update": [P, P, P, c_long, c_float, c_float, c_float, c_float, c_float, P, P, P],
     "iris_cfg_combine": [P, P, c_long, c_float, P, P],
     "iris_clamp": [P, c_long, c_float, c_float, P, P],
 }

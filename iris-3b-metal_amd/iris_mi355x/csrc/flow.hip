@@ -37,6 +37,27 @@ __global__ __launch_bounds__(256) void dpm1_kernel(const float* __restrict__ x, 
   x_next[i] = a - b;
 }
 
+// Second-order multistep update (first-order when x0_prev is null); also stores this step's
+// x0 for the next step's history.
+__global__ __launch_bounds__(256) void dpm_kernel(const float* __restrict__ x, const float* __restrict__ v,
+                                                  const float* __restrict__ x0_prev, long n, float s, float c_x,
+                                                  float c_x0, float c_d, float r0, float* __restrict__ x_next,
+                                                  float* __restrict__ x0_out) {
+  const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float xi = x[i];
+  const float x0 = xi - s * v[i];
+  if (x0_out) x0_out[i] = x0;
+  const float a = c_x * xi;
+  const float b = c_x0 * x0;
+  float r = a - b;
+  if (x0_prev) {
+    const float d = (x0 - x0_prev[i]) / r0;
+    r = r - c_d * d;
+  }
+  x_next[i] = r;
+}
+
 __global__ __launch_bounds__(256) void cfg_kernel(const float* __restrict__ u, const float* __restrict__ c, long n,
                                                   float scale, float* __restrict__ out) {
   const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
@@ -88,6 +109,18 @@ extern "C" int iris_dpm1_update(const float* x, const float* v, long n, float s,
   if (n == 0) return IRIS_OK;
   dpm1_kernel<<<blocks_for(n), 256, 0, stream>>>(x, v, n, s, c_x, c_x0, x_next);
   return check_launch("dpm1_update");
+}
+
+extern "C" int iris_dpm_update(const float* x, const float* v, const float* x0_prev, long n, float s, float c_x,
+                               float c_x0, float c_d, float r0, float* x_next, float* x0_out, hipStream_t stream) {
+  IRIS_REQUIRE(n >= 0 && x && v && x_next, "dpm_update: bad arguments");
+  IRIS_REQUIRE(!x0_prev || r0 != 0.0f, "dpm_update: the step ratio r0 must be nonzero");
+  IRIS_REQUIRE(x_next != x && x_next != v && (!x0_out || (x0_out != x && x0_out != v && x0_out != x_next)) &&
+                   (!x0_prev || (x0_prev != x_next && x0_prev != x0_out)),
+               "dpm_update: outputs must not alias the inputs or each other");
+  if (n == 0) return IRIS_OK;
+  dpm_kernel<<<blocks_for(n), 256, 0, stream>>>(x, v, x0_prev, n, s, c_x, c_x0, c_d, r0, x_next, x0_out);
+  return check_launch("dpm_update");
 }
 
 extern "C" int iris_cfg_combine(const float* v_uncond, const float* v_cond, long n, float scale, float* out,

@@ -487,6 +487,17 @@ def dpm1_update(x, v, s: float, c_x: float, c_x0: float, out) -> None:
            L.stream())
 
 
+def dpm_update(x, v, x0_prev, s: float, c_x: float, c_x0: float, c_d: float, r0: float, x_next, x0_out) -> None:
+    """One FlowDPMSolver step (src/iris3b/flow/solver.py:90-109): first order when ``x0_prev``
+    is None, else second order; ``x0_out`` receives this step's ``x0 = x - s*v``."""
+    tensors = [t for t in (x, v, x0_prev, x_next, x0_out) if t is not None]
+    _on_gpu(*tensors)
+    _require(all(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == x.numel() for t in tensors),
+             "dpm_update needs contiguous FP32 tensors of one size")
+    L.call("iris_dpm_update", L.ptr(x), L.ptr(v), L.ptr(x0_prev), x.numel(), float(s), float(c_x), float(c_x0),
+           float(c_d), float(r0), L.ptr(x_next), L.ptr(x0_out), L.stream())
+
+
 def cfg_combine(v_uncond, v_cond, scale: float, out) -> None:
     _on_gpu(v_uncond, v_cond, out)
     L.call("iris_cfg_combine", L.ptr(v_uncond), L.ptr(v_cond), v_cond.numel(), float(scale), L.ptr(out), L.stream())

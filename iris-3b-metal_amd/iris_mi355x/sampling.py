@@ -5,8 +5,9 @@
   one FP32 kernel per step in the reference's operation order, the time values are staged
   on the device before the loop, and the only host synchronisation is the finiteness check
   of the final sample.
-- ``dpm1_sample``: first-order ``FlowDPMSolver`` (flow-Euler in log-SNR form) with
-  classifier-free guidance (src/iris3b/flow/solver.py:36-141, ``order=1``).
+- ``dpm_sample``: the multistep ``FlowDPMSolver`` of the original route (order 2 by default,
+  order 1 = flow-Euler in log-SNR form) with classifier-free guidance and its interval
+  (src/iris3b/flow/solver.py:36-141); ``dpm1_sample`` is its first-order form.
 """
 
 from __future__ import annotations
@@ -60,10 +61,16 @@ def _lam(t: float) -> float:
 
 
 @torch.no_grad()
-def dpm1_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor | None = None, steps: int = 20,
-                shift: float = 4.0, cfg_scale: float = 3.0, cfg_interval: tuple[float, float] = (0.0, 1.0),
-                num_timesteps: int = 1000) -> torch.Tensor:
-    """First-order ``FlowDPMSolver.sample`` with CFG batching ``cat([uncond, cond])``."""
+def dpm_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor | None = None, steps: int = 50,
+               order: int = 2, shift: float = 1.0, cfg_scale: float = 1.0,
+               cfg_interval: tuple[float, float] = (0.0, 1.0), num_timesteps: int = 1000) -> torch.Tensor:
+    """``FlowDPMSolver.sample`` (src/iris3b/flow/solver.py:111-141) with v-prediction: multistep
+    DPM-Solver++ of order 1 or 2 (the order ramps up over the first steps and back to 1 at the
+    end), classifier-free guidance over the batch ``cat([uncond, cond])`` for the steps whose
+    start time lies inside ``cfg_interval`` (solver.py:58-74). Every update is one FP32 kernel
+    (``iris_dpm_update``) that also keeps the step's ``x0`` for the next one."""
+    if order not in (1, 2):
+        raise ValueError(f"order must be 1 or 2, got {order}")
     grid = time_grid(steps, shift)
     x = torch.empty(z.shape, device=cond.device, dtype=torch.float32)
     x.copy_(z)  # the loop writes its two latent buffers; the caller's z stays untouched
@@ -73,7 +80,9 @@ def dpm1_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor
     v = torch.empty_like(x)
     v2 = torch.empty_like(x2)
     x_next = torch.empty_like(x)
+    x0s = [torch.empty_like(x), torch.empty_like(x)]  # this step's x0 and the previous one
     flat = x.numel()
+    s_prev = None
     for i in range(1, steps + 1):
         s, t = grid[i - 1], grid[i]
         lo, hi = cfg_interval
@@ -87,7 +96,23 @@ def dpm1_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor
             K.cfg_combine(v2[:batch], v2[batch:], cfg_scale, v)
         else:
             model(x, t_model, cond, out=v)
-        phi1 = math.expm1(-(_lam(t) - _lam(s)))
-        K.dpm1_update(x, v, s, t / s, (1.0 - t) * phi1, x_next)
+        x0, x0_prev = x0s[i % 2], x0s[(i + 1) % 2]
+        if min(i, order, steps + 1 - i) == 1:
+            phi1 = math.expm1(-(_lam(t) - _lam(s)))
+            K.dpm_update(x, v, None, s, t / s, (1.0 - t) * phi1, 0.0, 1.0, x_next, x0)
+        else:  # solver.py:96-109 with (s1, x0_1) the previous step and (s0, x0_0) this one
+            lam_t, lam_0, lam_1 = _lam(t), _lam(s), _lam(s_prev)
+            h, h0 = lam_t - lam_0, lam_0 - lam_1
+            phi1 = math.expm1(-h)
+            K.dpm_update(x, v, x0_prev, s, t / s, (1.0 - t) * phi1, 0.5 * (1.0 - t) * phi1, h0 / h, x_next, x0)
+        s_prev = s
         x, x_next = x_next, x
     return x
+
+
+def dpm1_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor | None = None, steps: int = 20,
+                shift: float = 4.0, cfg_scale: float = 3.0, cfg_interval: tuple[float, float] = (0.0, 1.0),
+                num_timesteps: int = 1000) -> torch.Tensor:
+    """First-order ``FlowDPMSolver.sample`` (``dpm_sample`` with ``order=1``)."""
+    return dpm_sample(model, z, cond, uncond, steps=steps, order=1, shift=shift, cfg_scale=cfg_scale,
+                      cfg_interval=cfg_interval, num_timesteps=num_timesteps)

@@ -65,21 +65,22 @@ def test_released_turbo_matches_oracle_sampler(released):
     assert torch.equal(noise_d.cpu(), noise)  # the sampler keeps its own latent buffers
 
 
-def test_released_dpm1_cfg_matches_oracle_sampler(released):
-    """First-order FlowDPMSolver with classifier-free guidance (batch cat([uncond, cond])) and
-    a guidance interval that leaves the first step unguided."""
-    from iris_mi355x.sampling import dpm1_sample
+@pytest.mark.parametrize("order", [1, 2])
+def test_released_dpm_cfg_matches_oracle_sampler(released, order):
+    """FlowDPMSolver of order 1 and 2 with classifier-free guidance (batch cat([uncond, cond]))
+    and a guidance interval that leaves the first step unguided."""
+    from iris_mi355x.sampling import dpm_sample
 
     cfg, sd, engine = released
     g = torch.Generator().manual_seed(4)
     z = torch.randn(1, 3, 32, 32, generator=g)
     cond = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g)
     uncond = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g)
-    kw = dict(steps=4, shift=4.0, cfg_scale=3.0, cfg_interval=(0.0, 0.95))
-    want = O.dpm_sample(lambda x, t, y: O.forward(sd, cfg, x, t, prepared_text=y), z, cond, uncond, order=1, **kw)
+    kw = dict(steps=5, order=order, shift=4.0, cfg_scale=3.0, cfg_interval=(0.0, 0.95))
+    want = O.dpm_sample(lambda x, t, y: O.forward(sd, cfg, x, t, prepared_text=y), z, cond, uncond, **kw)
     z_d = z.to(DEV)
-    got = dpm1_sample(engine, z_d, cond.to(DEV), uncond.to(DEV), **kw)
-    check(got, want, "released dpm1 cfg")
+    got = dpm_sample(engine, z_d, cond.to(DEV), uncond.to(DEV), **kw)
+    check(got, want, f"released dpm{order} cfg")
     assert torch.equal(z_d.cpu(), z)
 
 

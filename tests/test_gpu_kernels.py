@@ -382,6 +382,38 @@ def test_flow_euler_is_bitwise_the_reference_update():
         assert torch.equal(xn.cpu(), want)
 
 
+def test_dpm_update_follows_the_solver_expressions():
+    """Both orders of the FlowDPMSolver update against the reference's tensor expressions
+    evaluated in FP32 on the CPU (solver.py:90-109): first order bit for bit; the second-order
+    divide by r0 may round differently from a multiply by its reciprocal (one ulp)."""
+    import math
+
+    g = gen(16)
+    x, v, x0_1 = (torch.randn(3, 64, 64, generator=g) for _ in range(3))
+    lam = lambda u: math.log((1.0 - u) / u)
+    s1, s0, t = 0.92, 0.80, 0.57
+    # first order
+    x0 = x - s0 * v
+    phi1 = math.expm1(-(lam(t) - lam(s0)))
+    want1 = (t / s0) * x - (1.0 - t) * phi1 * x0
+    xd, vd = x.to(DEV), v.to(DEV)
+    xn, x0o = torch.empty_like(xd), torch.empty_like(xd)
+    K.dpm_update(xd, vd, None, s0, t / s0, (1.0 - t) * phi1, 0.0, 1.0, xn, x0o)
+    assert torch.equal(x0o.cpu(), x0)
+    assert torch.equal(xn.cpu(), want1)
+    # second order
+    h, h0 = lam(t) - lam(s0), lam(s0) - lam(s1)
+    r0 = h0 / h
+    d = (x0 - x0_1) / r0
+    phi1 = math.expm1(-h)
+    want2 = (t / s0) * x - (1.0 - t) * phi1 * x0 - 0.5 * (1.0 - t) * phi1 * d
+    K.dpm_update(xd, vd, x0_1.to(DEV), s0, t / s0, (1.0 - t) * phi1, 0.5 * (1.0 - t) * phi1, r0, xn, x0o)
+    assert torch.equal(x0o.cpu(), x0)
+    torch.testing.assert_close(xn.cpu(), want2, rtol=2e-7, atol=1e-7)
+    with pytest.raises(ValueError, match="alias"):
+        K.dpm_update(xd, vd, None, s0, 1.0, 1.0, 0.0, 1.0, xd, x0o)
+
+
 def test_cfg_combine_and_clamp():
     g = gen(15)
     u, c = torch.randn(1000, generator=g), torch.randn(1000, generator=g)
