@@ -15,10 +15,14 @@
 // 8 x 4 block and share their operands through that XCD's L2.
 #include "iris_common.hpp"
 
+#include <type_traits>
+
 namespace iris {
 namespace {
 
 constexpr int kBK = 64;
+// word 3 of a raw buffer resource on gfx9-family GPUs (32-bit dwords, no swizzle)
+constexpr int kBufferFlags = 0x00020000;
 
 struct GemmGroup {
   const bf16* a;
@@ -68,6 +72,171 @@ __device__ __forceinline__ int swz(int r) {
   return (r / (16 / CPR)) % CPR;
 }
 
+// One workgroup's output tile: the logical tile id (XCD remap) picks the group, then groups
+// of 8 row tiles sweep all column tiles, so that the ~32 tiles running at once on one XCD form
+// an 8 x 4 block and share their operands through that XCD's L2.
+struct TileJob {
+  const bf16* a;
+  const bf16* b;
+  const float* bias;
+  void* c;
+  int m, tm, tn;
+};
+
+template <int BM, int BN>
+__device__ __forceinline__ TileJob locate_tile_at(const GemmArgs& p, int tile) {
+  const bool second = p.ngroups > 1 && tile >= p.g1.tile_begin;
+  const GemmGroup& gr = second ? p.g1 : p.g0;
+  tile -= second ? p.g1.tile_begin : 0;
+  const int tiles_n = (p.n + BN - 1) / BN;
+  constexpr int GM = 8;
+  const int group = tile / (GM * tiles_n);
+  const int gm = min(GM, gr.tiles_m - group * GM);
+  const int in_group = tile - group * GM * tiles_n;
+  return TileJob{gr.a, gr.b, gr.bias, gr.c, gr.m, group * GM + in_group % gm, in_group / gm};
+}
+
+template <int BM, int BN>
+__device__ __forceinline__ TileJob locate_tile(const GemmArgs& p) {
+  return locate_tile_at<BM, BN>(p, xcd_remap(blockIdx.x, p.total_tiles));
+}
+
+// Persistent workgroups: round r of a grid of G workgroups covers logical tiles r G .. r G +
+// G - 1, remapped per XCD as a one-round launch would be; -1 when this workgroup has no tile
+// in round r (only in the last one).
+__device__ __forceinline__ int persistent_tile(const GemmArgs& p, int round) {
+  const int G = gridDim.x;
+  const int base = round * G;
+  const int count = min(G, p.total_tiles - base);
+  return static_cast<int>(blockIdx.x) < count ? base + xcd_remap(blockIdx.x, count) : -1;
+}
+
+// Epilogue shared by the kernels: acc[i][j][r] = C[m, n] with n = tile + wave col + 32 i +
+// 8 (r / 4) + 4 g + r % 4, m = tile + wave row + 32 j + l32; BF16 output through the LDS ring.
+// `mid` runs once the accumulators are no longer needed (after they are staged in LDS, or at
+// the end for FP32 output); the persistent kernel issues its next loads there.
+template <int BM, int BN, int WM, int WN, int FM, int FN, int NW, int RING, int EPI, typename TC, typename Mid>
+__device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, const TileJob& job, int N, long ldc,
+                                           int wm, int wn, Mid&& mid) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  const int M = job.m, tm = job.tm, tn = job.tn;
+  const float* __restrict__ bias = job.bias;
+  TC* __restrict__ C = static_cast<TC*>(job.c);
+  if constexpr (sizeof(TC) == 2) {
+    // BF16 output: stage the tile through LDS (the K ring is free once every wave is past its
+    // last MFMA) so that each store instruction writes whole 512-byte row segments instead of
+    // 16-byte pieces of 32 rows. 4-element unit u of row r sits at unit u ^ 2 (r & MASK).
+    constexpr int OUT_N = EPI == IRIS_EPI_SILU_MUL ? BN / 2 : BN;
+    constexpr int UNITS = OUT_N / 4;
+    // the XOR must stay inside the row: within 32-unit blocks when the row holds whole ones,
+    // else within 16-unit blocks (rows of 48 units for BN = 192)
+    constexpr int MASK = UNITS % 32 == 0 ? 15 : (UNITS % 16 == 0 ? 7 : 0);
+    static_assert(UNITS % 16 == 0 || UNITS < 16, "output tile width");
+    static_assert(BM * OUT_N <= RING, "output tile must fit in the LDS ring");
+    bf16* cl = lds;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int r = wm * WM + j * 32 + l32;
+      bf16* crow_l = cl + r * OUT_N;
+      const int sw = 2 * (r & MASK);
+      if constexpr (EPI == IRIS_EPI_SILU_MUL) {
+#pragma unroll
+        for (int i = 0; i < FN; i += 2) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = silu(acc[i][j][4 * q + e]) * acc[i + 1][j][4 * q + e];
+            const int u = ((wn * WN + i * 32) / 2 + 8 * q + 4 * g) / 4;
+            store_out4(crow_l + 4 * (u ^ sw), v[0], v[1], v[2], v[3]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int nl = wn * WN + i * 32 + 8 * q + 4 * g;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
+            if (bias) {
+              const f32x4 bv = load4(bias + min(tn * BN + nl, N - 4));
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] += bv[e];
+            }
+            store_out4(crow_l + 4 * ((nl / 4) ^ sw), v[0], v[1], v[2], v[3]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    mid();
+    constexpr int CHUNKS = OUT_N / 8;  // 16-byte chunks per row
+    const int n_out = EPI == IRIS_EPI_SILU_MUL ? N / 2 : N;
+    const int col0 = tn * OUT_N;
+#pragma unroll 4
+    for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
+      const int r = idx / CHUNKS;
+      const int c = idx - r * CHUNKS;
+      const int m = tm * BM + r;
+      const int n0 = col0 + 8 * c;
+      if (m >= M || n0 >= n_out) continue;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * OUT_N + 8 * (c ^ (r & MASK)));
+      TC* dst = C + static_cast<long>(m) * ldc + n0;
+      if (n0 + 8 <= n_out) {
+        *reinterpret_cast<bf16x8*>(dst) = v;
+      } else {
+        *reinterpret_cast<bf16x4*>(dst) = bf16x4{v[0], v[1], v[2], v[3]};  // n_out % 4 == 0
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int m = tm * BM + wm * WM + j * 32 + l32;
+    if (m >= M) continue;
+    TC* crow = C + static_cast<long>(m) * ldc;
+    if constexpr (EPI == IRIS_EPI_SILU_MUL) {
+#pragma unroll
+      for (int i = 0; i < FN; i += 2) {
+        const int nbase = tn * BN + wn * WN + i * 32;
+        if (nbase >= N) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = silu(acc[i][j][4 * q + e]) * acc[i + 1][j][4 * q + e];
+          store_out4(crow + nbase / 2 + 8 * q + 4 * g, v[0], v[1], v[2], v[3]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n0 = tn * BN + wn * WN + i * 32 + 8 * q + 4 * g;
+          if (n0 >= N) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
+          if (bias) {
+            const f32x4 bv = load4(bias + n0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += bv[e];
+          }
+          store_out4(crow + n0, v[0], v[1], v[2], v[3]);
+        }
+      }
+    }
+  }
+  mid();
+}
+
 // Loads of part `part` when a K tile's lpw loads are dealt round-robin into `parts` parts.
 constexpr int part_loads(int lpw, int parts, int part) { return part < parts ? (lpw - part + parts - 1) / parts : 0; }
 
@@ -101,25 +270,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
   static_assert(PARTS >= 1 && PARTS <= 4 && PARTS <= KS && PARTS <= LPW, "load parts");
   __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
-  int tile = xcd_remap(blockIdx.x, p.total_tiles);
-  const bool second = p.ngroups > 1 && tile >= p.g1.tile_begin;
-  const bf16* __restrict__ A = second ? p.g1.a : p.g0.a;
-  const bf16* __restrict__ B = second ? p.g1.b : p.g0.b;
-  const float* __restrict__ bias = second ? p.g1.bias : p.g0.bias;
-  TC* __restrict__ C = static_cast<TC*>(second ? p.g1.c : p.g0.c);
-  const int M = second ? p.g1.m : p.g0.m;
-  const int tiles_m = second ? p.g1.tiles_m : p.g0.tiles_m;
-  tile -= second ? p.g1.tile_begin : 0;
-  const int N = p.n;
-  const int tiles_n = (N + BN - 1) / BN;
-  // groups of 8 row tiles sweep all column tiles: ~32 concurrent tiles of one XCD form an
-  // 8 x 4 block, so both operands are re-read from that XCD's L2
-  constexpr int GM = 8;
-  const int group = tile / (GM * tiles_n);
-  const int gm = min(GM, tiles_m - group * GM);
-  const int in_group = tile - group * GM * tiles_n;
-  const int tm = group * GM + in_group % gm;
-  const int tn = in_group / gm;
+  const TileJob job = locate_tile<BM, BN>(p);
+  const bf16* __restrict__ A = job.a;
+  const bf16* __restrict__ B = job.b;
+  const int M = job.m, N = p.n, tm = job.tm, tn = job.tn;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -260,115 +414,218 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
   }
   wait_vmcnt<0>();
 
-  // epilogue: acc[i][j][r] = C[m, n] with n = tile + 8 (r / 4) + 4 g + r % 4, m = tile + l32
-  const long ldc = p.ldc;
-  if constexpr (sizeof(TC) == 2) {
-    // BF16 output: stage the tile through LDS (the K ring is free once every wave is past its
-    // last MFMA) so that each store instruction writes whole 512-byte row segments instead of
-    // 16-byte pieces of 32 rows. 4-element unit u of row r sits at unit u ^ 2 (r & MASK).
-    constexpr int OUT_N = EPI == IRIS_EPI_SILU_MUL ? BN / 2 : BN;
-    constexpr int UNITS = OUT_N / 4;
-    // the XOR must stay inside the row: within 32-unit blocks when the row holds whole ones,
-    // else within 16-unit blocks (rows of 48 units for BN = 192)
-    constexpr int MASK = UNITS % 32 == 0 ? 15 : (UNITS % 16 == 0 ? 7 : 0);
-    static_assert(UNITS % 16 == 0 || UNITS < 16, "output tile width");
-    static_assert(BM * OUT_N <= STAGES * STAGE, "output tile must fit in the LDS ring");
-    bf16* cl = lds;
-    __syncthreads();
+  store_tile<BM, BN, WM, WN, FM, FN, NW, STAGES * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, [] {});
+}
+
+// Instruction order of one k-step of gemm_w4_kernel: an MFMA, then the next k-step's NR
+// fragment reads each followed by an MFMA, then W LDS writes and L global loads alternating
+// with MFMAs while they last, then the rest of the NM MFMAs.
+template <int NR, int NM, int W, int L>
+__device__ __forceinline__ void order_w4() {
+  static_assert(1 + NR + (W > L ? W : L) <= NM, "MFMAs per k-step");
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-      const int r = wm * WM + j * 32 + l32;
-      bf16* crow_l = cl + r * OUT_N;
-      const int sw = 2 * (r & MASK);
-      if constexpr (EPI == IRIS_EPI_SILU_MUL) {
-#pragma unroll
-        for (int i = 0; i < FN; i += 2) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = silu(acc[i][j][4 * q + e]) * acc[i + 1][j][4 * q + e];
-            const int u = ((wn * WN + i * 32) / 2 + 8 * q + 4 * g) / 4;
-            store_out4(crow_l + 4 * (u ^ sw), v[0], v[1], v[2], v[3]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int nl = wn * WN + i * 32 + 8 * q + 4 * g;
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
-            if (bias) {
-              const f32x4 bv = load4(bias + min(tn * BN + nl, N - 4));
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] += bv[e];
-            }
-            store_out4(crow_l + 4 * ((nl / 4) ^ sw), v[0], v[1], v[2], v[3]);
-          }
-        }
-      }
-    }
-    __syncthreads();
-    constexpr int CHUNKS = OUT_N / 8;  // 16-byte chunks per row
-    const int n_out = EPI == IRIS_EPI_SILU_MUL ? N / 2 : N;
-    const int col0 = tn * OUT_N;
-#pragma unroll 4
-    for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
-      const int r = idx / CHUNKS;
-      const int c = idx - r * CHUNKS;
-      const int m = tm * BM + r;
-      const int n0 = col0 + 8 * c;
-      if (m >= M || n0 >= n_out) continue;
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * OUT_N + 8 * (c ^ (r & MASK)));
-      TC* dst = C + static_cast<long>(m) * ldc + n0;
-      if (n0 + 8 <= n_out) {
-        *reinterpret_cast<bf16x8*>(dst) = v;
-      } else {
-        *reinterpret_cast<bf16x4*>(dst) = bf16x4{v[0], v[1], v[2], v[3]};  // n_out % 4 == 0
-      }
-    }
-    return;
+  for (int i = 0; i < NR; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   }
+  constexpr int X = W > L ? W : L;
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int m = tm * BM + wm * WM + j * 32 + l32;
-    if (m >= M) continue;
-    TC* crow = C + static_cast<long>(m) * ldc;
-    if constexpr (EPI == IRIS_EPI_SILU_MUL) {
+  for (int i = 0; i < X; ++i) {
+    if (i < W) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+    if (i < L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+  if constexpr (NM - 1 - NR - X > 0) __builtin_amdgcn_sched_group_barrier(0x008, NM - 1 - NR - X, 0);
+}
+
+// Four waves (one per SIMD), each owning a 128 x 128 block of a 256 x 256 tile, with register
+// staged refills: every wave loads its quarter of K tile t + 2 from global memory into
+// registers (16-byte loads that do not hold up the wave, unlike global_load_lds) while it
+// multiplies tile t, and writes tile t + 1, loaded one K tile earlier, into the free LDS
+// stage. A 128 x 128 block per wave reads half as many LDS bytes per MFMA as 128 x 64; the
+// accumulators live in the AGPRs. Inside each k-step the fragment reads of the next k-step,
+// then this k-step's share of the LDS writes and global loads, are spread between the MFMAs.
+template <int EPI, typename TC, bool PERSIST>
+__global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
+  constexpr int BM = 256, BN = 256, BK = 64, NW = 4;
+  constexpr int WM = 128, WN = 128, FM = 4, FN = 4;
+  constexpr int KS = BK / 16;
+  constexpr int CPR = BK / 8;
+  constexpr int RPL = 64 / CPR;                // rows per 1 KB wave load
+  constexpr int A_LOADS = BM / RPL / NW;       // 8
+  constexpr int B_LOADS = BN / RPL / NW;       // 8
+  constexpr int LW = A_LOADS + B_LOADS;        // 16 loads of 16 bytes per lane per K tile
+  constexpr int LPS = LW / KS;                 // global loads per k-step
+  constexpr int NR = FN + FM, NM = FN * FM;    // fragment reads and MFMAs per k-step
+  constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
+  static_assert(LW % KS == 0 && KS == 4, "loads per k-step");
+  __shared__ __attribute__((aligned(1024))) bf16 lds[2 * STAGE];
+
+  int cur_tile = persistent_tile(p, 0);
+  if (cur_tile < 0) return;
+  TileJob job = locate_tile_at<BM, BN>(p, cur_tile);
+  const int N = p.n;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  const int w = tid >> 6;
+  const int wm = w >> 1, wn = w & 1;
+
+  // load i: A rows (8 w + i) * RPL .. + RPL for i < 8, B rows (8 w + i - 8) * RPL .. for the rest;
+  // lane l fetches the chunk that belongs at byte 16 l of that 1 KB block in LDS
+  const int ld_r = lane / CPR;
+  const int ld_p = lane % CPR;
+  int off[LW];
+  auto set_offsets = [&](const TileJob& jb) {
 #pragma unroll
-      for (int i = 0; i < FN; i += 2) {
-        const int nbase = tn * BN + wn * WN + i * 32;
-        if (nbase >= N) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = silu(acc[i][j][4 * q + e]) * acc[i + 1][j][4 * q + e];
-          store_out4(crow + nbase / 2 + 8 * q + 4 * g, v[0], v[1], v[2], v[3]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < FN; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n0 = tn * BN + wn * WN + i * 32 + 8 * q + 4 * g;
-          if (n0 >= N) continue;
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
-          if (bias) {
-            const f32x4 bv = load4(bias + n0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] += bv[e];
-          }
-          store_out4(crow + n0, v[0], v[1], v[2], v[3]);
-        }
-      }
+    for (int i = 0; i < LW; ++i) {
+      const bool is_a = i < A_LOADS;
+      const int r = (w * A_LOADS + (is_a ? i : i - A_LOADS)) * RPL + ld_r;
+      off[i] = is_a ? min(jb.tm * BM + r, jb.m - 1) * static_cast<int>(p.lda) + 8 * (ld_p ^ swz<BK>(r))
+                    : min(jb.tn * BN + r, N - 1) * static_cast<int>(p.ldb) + 8 * (ld_p ^ swz<BK>(r));
     }
+  };
+  set_offsets(job);
+  auto dst = [&](int i) {  // element offset inside a stage
+    return (i < A_LOADS ? (w * A_LOADS + i) * RPL * BK : A_STAGE + (w * B_LOADS + i - A_LOADS) * RPL * BK) + 8 * lane;
+  };
+  // one register slot per load: slot i of K tile t + 1 is written to LDS before slot i of
+  // K tile t + 2 is loaded into it
+  bf16x8 staged[LW];
+  // buffer loads: the per-load 32-bit byte offset is the only VGPR an address costs, the K
+  // position goes in an SGPR, and reads past the operand return zeros instead of faulting
+  __amdgpu_buffer_rsrc_t rsrc_a, rsrc_b;
+  auto set_rsrc = [&](const TileJob& jb) {
+    rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void*)jb.a, (short)0, jb.m * static_cast<int>(p.lda) * 2, kBufferFlags);
+    rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void*)jb.b, (short)0, N * static_cast<int>(p.ldb) * 2, kBufferFlags);
+  };
+  set_rsrc(job);
+  auto gload = [&](int kt, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+      staged[i] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(i < A_LOADS ? rsrc_a : rsrc_b, off[i] * 2, kt * BK * 2, 0));
+  };
+  auto lwrite = [&](int stage, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) *reinterpret_cast<bf16x8*>(lds + stage * STAGE + dst(i)) = staged[i];
+  };
+
+  int a_row[FM], b_row[FN];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) a_row[j] = wm * WM + j * 32 + l32;
+#pragma unroll
+  for (int i = 0; i < FN; ++i) b_row[i] = wn * WN + i * 32 + l32;
+  bf16x8 wf[2][FN], xf[2][FM];
+  auto read_frags = [&](int stage, int ks, int buf) {
+    const bf16* sa = lds + stage * STAGE;
+    const bf16* sb = sa + A_STAGE;
+    const int c = 2 * ks + g;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+      wf[buf][i] = *reinterpret_cast<const bf16x8*>(sb + b_row[i] * BK + 8 * (c ^ swz<BK>(b_row[i])));
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+      xf[buf][j] = *reinterpret_cast<const bf16x8*>(sa + a_row[j] * BK + 8 * (c ^ swz<BK>(a_row[j])));
+  };
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
+  auto mfmas = [&](int cur) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[cur][i], xf[cur][j], acc[i][j], 0, 0, 0);
+  };
+
+  // K tile t: multiplied from LDS stage t % 2. Its first three k-steps write tile t + 1
+  // (loaded during tile t - 1) into stage (t + 1) % 2, six, five and five 1 KB blocks; its
+  // four k-steps load a quarter of tile t + 2 each into slots already written. The barrier
+  // before the last k-step publishes the writes and retires stage t % 2. Past the end the
+  // loads repeat the last K tile; nothing writes them to LDS.
+  constexpr int W0 = 6, W1 = 11;  // LDS-write split points
+  const int KT = p.k / BK;
+  gload(0, 0, LW);
+  for (int round = 0;; ++round) {
+  lwrite(0, 0, LW);  // K tile 0, loaded before the previous tile's epilogue (or just above)
+  gload(min(1, KT - 1), 0, LW);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __syncthreads();
+  read_frags(0, 0, 0);
+
+  auto ktile = [&](int t, auto P) {  // t + 1 < KT, P = t % 2 as a compile-time constant
+    constexpr int S = decltype(P)::value;
+    const int t2 = min(t + 2, KT - 1);
+    // k-step 0
+    read_frags(S, 1, 1);
+    lwrite(S ^ 1, 0, W0);
+    gload(t2, 0, LPS);
+    mfmas(0);
+    order_w4<NR, NM, W0, LPS>();
+    // k-step 1
+    read_frags(S, 2, 0);
+    lwrite(S ^ 1, W0, W1);
+    gload(t2, LPS, 2 * LPS);
+    mfmas(1);
+    order_w4<NR, NM, W1 - W0, LPS>();
+    // k-step 2
+    read_frags(S, 3, 1);
+    lwrite(S ^ 1, W1, LW);
+    gload(t2, 2 * LPS, 3 * LPS);
+    mfmas(0);
+    order_w4<NR, NM, LW - W1, LPS>();
+    // k-step 3: publish tile t + 1, then read its first fragments behind the last MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes and reads are done
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(S ^ 1, 0, 0);
+    gload(t2, 3 * LPS, LW);
+    mfmas(1);
+    order_w4<NR, NM, 0, LPS>();
+  };
+  int t = 0;
+  for (; t + 2 < KT; t += 2) {
+    ktile(t, std::integral_constant<int, 0>{});
+    ktile(t + 1, std::integral_constant<int, 1>{});
+  }
+  if (t + 1 < KT) {
+    ktile(t, std::integral_constant<int, 0>{});
+    ++t;
+  }
+  {  // last K tile, stage t % 2
+    const int S = t & 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KS) read_frags(S, ks + 1, cur ^ 1);
+      mfmas(cur);
+    }
+  }
+  wait_vmcnt<0>();  // the repeated loads of the last K tile
+  // the next tile's first K tile is in flight while this tile's output goes out
+  const int next_tile = PERSIST ? persistent_tile(p, round + 1) : -1;
+  const TileJob next = next_tile >= 0 ? locate_tile_at<BM, BN>(p, next_tile) : job;
+  store_tile<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, [&] {
+    if (next_tile >= 0) {
+      set_rsrc(next);
+      set_offsets(next);
+      gload(0, 0, LW);
+    }
+  });
+  if (next_tile < 0) break;
+  __syncthreads();  // every wave is done with the staged output before stage 0 is rewritten
+  job = next;
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
   }
 }
 
@@ -395,8 +652,45 @@ int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   return check_launch("gemm_bf16");
 }
 
+// Compute units of the current device (the persistent kernels launch one workgroup per CU).
+int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    cached[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0
+                      ? cus
+                      : 256;
+  }
+  return cached[dev];
+}
+
+// Plain BF16 output runs persistently (one workgroup per CU, the next tile's first K tile
+// loaded while the current tile is stored); the SwiGLU and FP32 epilogues keep one tile per
+// workgroup, since the register allocator spills inside the K loop when their epilogue shares
+// the persistent loop with it.
+int launch_w4(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
+  const int cus = device_cus();
+  const dim3 all(args.total_tiles);
+  if (epilogue == IRIS_EPI_SILU_MUL) {
+    if (c_dtype == IRIS_BF16)
+      gemm_w4_kernel<IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, 0, stream>>>(args);
+    else
+      gemm_w4_kernel<IRIS_EPI_SILU_MUL, float, false><<<all, 256, 0, stream>>>(args);
+  } else {
+    if (c_dtype == IRIS_BF16)
+      gemm_w4_kernel<IRIS_EPI_NONE, bf16, true><<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, 0,
+                                                   stream>>>(args);
+    else
+      gemm_w4_kernel<IRIS_EPI_NONE, float, false><<<all, 256, 0, stream>>>(args);
+  }
+  return check_launch("gemm_bf16");
+}
+
 struct TileShape {
   int bm, bn, bk, stages, wgm, wgn, parts;
+  bool w4 = false;  // gemm_w4_kernel: four waves of 128 x 128, register-staged refills
   bool swiglu() const { return (bn / wgn / 32) % 2 == 0; }
 };
 // BM x BN output tile, BK-deep K tiles in a ring of `stages`, wgm x wgn waves, the refill of a
@@ -413,28 +707,34 @@ constexpr TileShape kTiles[] = {
     {256, 256, 32, 4, 2, 4, 2},  // 8
     {256, 256, 64, 2, 2, 2, 1},  // 9: one wave per SIMD
     {256, 256, 64, 2, 2, 2, 2},  // 10
+    {256, 256, 64, 2, 2, 2, 1, true},  // 11: gemm_w4_kernel
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
 template <int I>
 int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   constexpr TileShape t = kTiles[I];
-  return launch_tile<t.bm, t.bn, t.bk, t.stages, t.wgm, t.wgn, t.parts>(args, c_dtype, epilogue, stream);
+  if constexpr (t.w4) {
+    static_assert(t.bm == 256 && t.bn == 256 && t.bk == 64, "gemm_w4_kernel tile");
+    return launch_w4(args, c_dtype, epilogue, stream);
+  } else {
+    return launch_tile<t.bm, t.bn, t.bk, t.stages, t.wgm, t.wgn, t.parts>(args, c_dtype, epilogue, stream);
+  }
 }
 
 // Tile shape: the candidate with the least estimated time, rounds of workgroups over the
 // 256 CUs (the last round costs as much as a full one) x tile area / relative per-CU rate.
-// Rates were measured on the trunk and pixel-stage shapes (sustained runs, refills in two
-// parts): 256x256 / 8 waves 1.0, 192x256 0.98, 256x192 0.96, 128x128 at two workgroups per
-// CU 0.9. The SwiGLU epilogue excludes the 192-column tile.
+// Rates were measured on the trunk and pixel-stage shapes (sustained runs): 256x256 with four
+// 128x128 waves 1.05, with eight 128x64 waves 1.0, 192x256 0.98, 256x192 0.96, 128x128 at two
+// workgroups per CU 0.9. The SwiGLU epilogue excludes the 192-column tile.
 int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
   if (forced >= 0) return forced;
   struct Candidate {
     int tile, per_cu;
     double rate;
   };
-  const Candidate candidates[] = {{1, 1, 1.0}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
-  int best = 1;
+  const Candidate candidates[] = {{11, 1, 1.05}, {1, 1, 1.0}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
+  int best = 11;
   double best_cost = 0.0;
   for (const Candidate& c : candidates) {
     const TileShape t = kTiles[c.tile];
@@ -507,7 +807,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   args.total_tiles = begin;
   if (begin == 0) return IRIS_OK;
   IRIS_REQUIRE(epilogue != IRIS_EPI_SILU_MUL || shape.swiglu(), "gemm: tile %dx%d has no SwiGLU epilogue", bm, bn);
-  static_assert(kNumTiles == 11, "one case per tile shape");
+  static_assert(kNumTiles == 12, "one case per tile shape");
   switch (tile) {
 #define IRIS_TILE_CASE(I) \
   case I:                 \
@@ -523,6 +823,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
     IRIS_TILE_CASE(8)
     IRIS_TILE_CASE(9)
     IRIS_TILE_CASE(10)
+    IRIS_TILE_CASE(11)
 #undef IRIS_TILE_CASE
     default:
       return fail(IRIS_E_INVALID, "gemm: no tile shape %d", tile);

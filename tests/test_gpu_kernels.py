@@ -149,7 +149,7 @@ def _gemm_ref(a, w, bias=None):
     return out if bias is None else out + bias.cpu()
 
 
-@pytest.mark.parametrize("tile", list(range(-1, 11)))
+@pytest.mark.parametrize("tile", list(range(-1, 12)))
 @pytest.mark.parametrize("mnk", [(300, 320, 128), (4096, 1280, 256), (1, 64, 64), (513, 260, 192)])
 def test_gemm_matches_fp32_reference(tile, mnk):
     m, n, k = mnk
@@ -180,7 +180,7 @@ def test_gemm_trunk_shapes(shape):
     torch.testing.assert_close(out[rows].cpu(), want, rtol=1e-4, atol=2e-4)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 4, 5, 6, 7, 8, 9, 10, 11])
 def test_gemm_swiglu_epilogue_and_grouped_streams(tile):
     d, hidden = 256, 682
     hp = 704
