@@ -92,9 +92,10 @@ int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int
                     long out_batch_rows0, long out_batch_rows1, const void* gate0, const void* gate1, long ld_gate,
                     long gate_batch_rows0, long gate_batch_rows1, hipStream_t stream);
 
-/* Tuning hook for the benchmark sweep: force the attention variant (0: 64 query rows per wave,
- * 2 stages of 64 keys; 1: 64 rows, 3 x 64 keys; 2: 32 rows, 2 x 64 keys; 3: 32 rows, 4 x 32 keys;
- * 4: 32 rows, 3 x 32 keys) or restore the automatic choice (-1).
+/* Tuning hook for the benchmark sweep: force the attention variant (32 query rows per wave in
+ * all; 0: 64-key tiles staged through registers, 1: 32-key tiles staged through registers,
+ * 2: 64-key tiles in a 2-stage global_load_lds ring, 3: 32-key tiles in a 3-stage ring) or
+ * restore the automatic choice (-1).
  * No counterpart in the reference. */
 int iris_flash_attn_force_variant(int variant);
 

@@ -27,6 +27,8 @@ namespace iris {
 namespace {
 
 constexpr int kHd = 128;
+// word 3 of a raw buffer resource on gfx9-family GPUs (32-bit dwords, no swizzle)
+constexpr int kBufferFlags = 0x00020000;
 
 struct AttnArgs {
   const bf16* q;
@@ -58,7 +60,43 @@ __device__ __forceinline__ int swz(int r) {
   return (r / (16 / CPR)) % CPR;
 }
 
-template <int QB, int STAGES, int KVT>
+// Store of one query row: lane owns query `row` and dims db*32 + 8 j + 4 g + (0..3) of head h;
+// out = o / l, times sigmoid(gate) when a gate is given; rows past n_split go to out1.
+__device__ __forceinline__ void store_row(const AttnArgs& p, const f32x16 (&o)[4], float l_lane, int b, int h, int row,
+                                          int g) {
+  const float l = l_lane + __shfl_xor(l_lane, 32);
+  const float inv = 1.0f / l;
+  if (row >= p.n) return;
+  const bool first = row < p.n_split;
+  bf16* out = first ? p.out0 : p.out1;
+  const bf16* gate = first ? p.gate0 : p.gate1;
+  const long r = first ? row : row - p.n_split;
+  if (out == nullptr) return;
+  bf16* orow_ptr = out + (b * (first ? p.out_brows0 : p.out_brows1) + r) * p.ld_out + h * kHd;
+  const bf16* grow_ptr = gate ? gate + (b * (first ? p.gate_brows0 : p.gate_brows1) + r) * p.ld_gate + h * kHd : nullptr;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d0 = db * 32 + 8 * j + 4 * g;
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = o[db][4 * j + e] * inv;
+      if (grow_ptr) {
+        const f32x4 gv = load4(grow_ptr + d0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] *= sigmoid(gv[e]);
+      }
+      store4(orow_ptr + d0, v);
+    }
+  }
+}
+
+// STAGED: K/V tiles travel global -> registers (16-byte buffer loads, which do not hold up the
+// wave as global_load_lds does) -> LDS (ds_write_b128) through two LDS stages: tile t + 1 is
+// written while tile t is multiplied, tile t + 2 is loaded meanwhile. Otherwise a ring of
+// STAGES tiles filled by global_load_lds.
+template <int QB, int STAGES, int KVT, bool STAGED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2 : 1))) void flash_attn_kernel(
     AttnArgs p) {  // 32-row waves: two workgroups per CU (<= 256 registers per lane)
   constexpr int KB = KVT / 32;     // 32-key blocks per tile
@@ -69,7 +107,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
   constexpr int VCPR = KVT / 8;    // 16-byte chunks per V^T row
   constexpr int VRPL = 64 / VCPR;  // V^T rows per 1 KB load
   static_assert(KVT == 32 || KVT == 64, "K/V tile of 32 or 64 keys");
-  static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64, "pipeline depth");
+  static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64 && (!STAGED || STAGES == 2), "pipeline depth");
   __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
   // logical workgroup: (b, kv head, head group) major, query block minor; the XCD remap keeps
@@ -125,6 +163,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
       __builtin_amdgcn_global_load_lds((const void*)(vt + v_off[j]), (void*)(vl + (w * LOADS + j) * 512), 16, 0, 0);
     }
   };
+  // register-staged path: lane l's 16 bytes of load j land at byte 16 l of the same 1 KB blocks
+  bf16x8 kreg[LOADS], vreg[LOADS];
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      kreg[j] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off[j] * 2, t * KVT * kHd * 2, 0));
+      vreg[j] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, v_off[j] * 2, t * KVT * 2, 0));
+    }
+  };
+  auto lwrite = [&](int stage) {
+    bf16* kl = lds + stage * STAGE;
+    bf16* vl = kl + TILE;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      *reinterpret_cast<bf16x8*>(kl + (w * LOADS + j) * 512 + 8 * lane) = kreg[j];
+      *reinterpret_cast<bf16x8*>(vl + (w * LOADS + j) * 512 + 8 * lane) = vreg[j];
+    }
+  };
 
   f32x16 o[4][QB];
 #pragma unroll
@@ -137,16 +197,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
   const float sl2 = p.scale_log2;
 
   const int n_tiles = (p.n + KVT - 1) / KVT;
+  if constexpr (STAGED) {
+    gload(0);
+    lwrite(0);
+    gload(min(1, n_tiles - 1));
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): tile 0 written
+    __builtin_amdgcn_s_barrier();
+  } else {
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < n_tiles) issue(s, s);
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < n_tiles) issue(s, s);
+  }
   for (int t = 0; t < n_tiles; ++t) {
-    if (t + STAGES - 2 < n_tiles)
-      wait_vmcnt<(STAGES - 2) * LPW>();
-    else
-      wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();  // tile t visible; stage (t-1) % STAGES no longer read
-    if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+    if constexpr (STAGED) {
+      // tile t + 1 (loaded during tile t - 1) into the stage tile t - 1 used, then load tile
+      // t + 2; past the end both repeat the last tile into a stage nothing reads again
+      lwrite((t + 1) & 1);
+      gload(min(t + 2, n_tiles - 1));
+    } else {
+      if (t + STAGES - 2 < n_tiles)
+        wait_vmcnt<(STAGES - 2) * LPW>();
+      else
+        wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();  // tile t visible; stage (t-1) % STAGES no longer read
+      if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+    }
     const bf16* kl = lds + (t % STAGES) * STAGE;
     const bf16* vl = kl + TILE;
 
@@ -235,48 +310,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
         }
       }
     }
+    if constexpr (STAGED) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): tile t + 1 written, tile t's reads done
+      __builtin_amdgcn_s_barrier();
+    }
   }
+  if constexpr (STAGED) wait_vmcnt<0>();  // the repeated loads past the last tile
 
-  // epilogue: lane owns query q0 + qb*32 + l32 and dims db*32 + 8 j + 4 g + (0..3)
+  // epilogue: lane owns query q0 + qb*32 + l32
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    const float l = l_run[qb] + __shfl_xor(l_run[qb], 32);
-    const float inv = 1.0f / l;
-    const int row = q0 + qb * 32 + l32;
-    if (row >= p.n) continue;
-    const bool first = row < p.n_split;
-    bf16* out = first ? p.out0 : p.out1;
-    const bf16* gate = first ? p.gate0 : p.gate1;
-    const long r = first ? row : row - p.n_split;
-    if (out == nullptr) continue;
-    bf16* orow_ptr = out + (b * (first ? p.out_brows0 : p.out_brows1) + r) * p.ld_out + h * kHd;
-    const bf16* grow_ptr =
-        gate ? gate + (b * (first ? p.gate_brows0 : p.gate_brows1) + r) * p.ld_gate + h * kHd : nullptr;
+    f32x16 oq[4];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d0 = db * 32 + 8 * j + 4 * g;
-        f32x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = o[db][qb][4 * j + e] * inv;
-        if (grow_ptr) {
-          const f32x4 gv = load4(grow_ptr + d0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] *= sigmoid(gv[e]);
-        }
-        store4(orow_ptr + d0, v);
-      }
-    }
+    for (int db = 0; db < 4; ++db) oq[db] = o[db][qb];
+    store_row(p, oq, l_run[qb], b, h, q0 + qb * 32 + l32, g);
   }
 }
 
 struct Variant {
   int qb, stages, kvt;
+  bool staged;
 };
-// 0: 64 query rows per wave, 2 stages of 64 keys; 1: 64 rows, 3 x 64 keys; 2: 32 rows,
-// 2 x 64 keys; 3: 32 rows, 4 x 32 keys; 4: 32 rows, 3 x 32 keys
-constexpr Variant kVariants[] = {{2, 2, 64}, {2, 3, 64}, {1, 2, 64}, {1, 4, 32}, {1, 3, 32}};
+// 0: 32 query rows per wave, 64-key tiles staged through registers; 1: the same with 32-key
+// tiles; 2: 64-key tiles, 2-stage global_load_lds ring; 3: 32-key tiles, 3-stage ring.
+// (An eight-wave ping-pong of MFMA and softmax phases measured 1.8x slower at the trunk shape
+// and was dropped.)
+constexpr Variant kVariants[] = {{1, 2, 64, true}, {1, 2, 32, true}, {1, 2, 64, false}, {1, 3, 32, false}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 int g_attn_variant = -1;
 
@@ -326,7 +385,7 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   args.hpw = group < 4 ? group : 4;
   // 32-row waves at two workgroups per CU measured fastest at every Iris shape (trunk 4352 and
   // 1280 tokens, pixel 4096): the softmax of one workgroup overlaps the MFMAs of the other.
-  const int variant = g_attn_variant >= 0 ? g_attn_variant : 2;
+  const int variant = g_attn_variant >= 0 ? g_attn_variant : 0;
   const Variant v = kVariants[variant];
   args.rows_per_wg = 32 * v.qb * 4 / args.hpw;
   args.n_qblocks = static_cast<int>((n + args.rows_per_wg - 1) / args.rows_per_wg);
@@ -338,19 +397,16 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   const dim3 grid(args.total_wg);
   switch (variant) {
     case 0:
-      flash_attn_kernel<2, 2, 64><<<grid, 256, 0, stream>>>(args);
+      flash_attn_kernel<1, 2, 64, true><<<grid, 256, 0, stream>>>(args);
       break;
     case 1:
-      flash_attn_kernel<2, 3, 64><<<grid, 256, 0, stream>>>(args);
+      flash_attn_kernel<1, 2, 32, true><<<grid, 256, 0, stream>>>(args);
       break;
     case 2:
-      flash_attn_kernel<1, 2, 64><<<grid, 256, 0, stream>>>(args);
-      break;
-    case 3:
-      flash_attn_kernel<1, 4, 32><<<grid, 256, 0, stream>>>(args);
+      flash_attn_kernel<1, 2, 64, false><<<grid, 256, 0, stream>>>(args);
       break;
     default:
-      flash_attn_kernel<1, 3, 32><<<grid, 256, 0, stream>>>(args);
+      flash_attn_kernel<1, 3, 32, false><<<grid, 256, 0, stream>>>(args);
       break;
   }
   return check_launch("flash_attn");
