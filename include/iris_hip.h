@@ -27,7 +27,7 @@ extern "C" {
 enum { IRIS_OK = 0, IRIS_E_INVALID = -1, IRIS_E_LAUNCH = -2, IRIS_E_UNSUPPORTED = -3 };
 enum { IRIS_F32 = 0, IRIS_BF16 = 1 };
 /* GEMM epilogues (bias is a separate optional pointer and is added first). */
-enum { IRIS_EPI_NONE = 0, IRIS_EPI_SILU_MUL = 1 };
+enum { IRIS_EPI_NONE = 0, IRIS_EPI_SILU_MUL = 1, IRIS_EPI_SILU = 2 };
 /* Activations of the GEMV input / output. */
 enum { IRIS_ACT_NONE = 0, IRIS_ACT_SILU = 1 };
 
@@ -99,16 +99,50 @@ int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int
  * No counterpart in the reference. */
 int iris_flash_attn_force_variant(int variant);
 
+/* The text refiner's masked attention (SelfAttention.forward with attn_mask = mask | eye,
+ * src/iris3b/nn/attention.py:117-132, src/iris3b/nn/embeddings.py:196-205): as iris_flash_attn
+ * with n_split = 0 and no gate, except that query q of batch b attends key j < n only where
+ * key_mask[b * n_pad + j] != 0 or j == q. key_mask: [batch, n_pad] bytes, 4-byte aligned (as
+ * written by iris_text_key_mask). Output row r of batch b goes to out row b*out_batch_rows + r. */
+int iris_flash_attn_masked(const void* q, const void* k, const void* vt, int batch, int heads, int kv_heads, long n,
+                           long n_pad, float scale, const void* key_mask, void* out, long ld_out, long out_batch_rows,
+                           hipStream_t stream);
+
+/* mask.bool() of the encoder's [batch, >= n] attention mask (row stride ld elements) as the
+ * [batch, n_pad] 0/1 bytes iris_flash_attn_masked reads (src/iris3b/nn/embeddings.py:199);
+ * elem_kind: 0 bool / uint8, 1 int32, 2 float32, 3 int64; bytes n .. n_pad - 1 are 0. */
+int iris_text_key_mask(const void* mask, int elem_kind, long ld, int batch, long n, long n_pad, void* out,
+                       hipStream_t stream);
+
+/* Self-attention of each text token over its encoder-layer states (LayerwiseAttentionBlock's
+ * SelfAttention without QK norm or RoPE, src/iris3b/nn/embeddings.py:110-141,
+ * src/iris3b/nn/attention.py:117-132): qkv BF16 [seqs * seq_len, 3 * heads * head_dim] (q | k |
+ * v, head-major inside each) -> out BF16 [seqs * seq_len, heads * head_dim], FP32 softmax with
+ * the given scale. seq_len <= 16, head_dim <= 128. */
+int iris_layer_attention(const void* qkv, void* out, long seqs, int seq_len, int heads, int head_dim, float scale,
+                         hipStream_t stream);
+
+/* The learned pool over encoder layers (LayerwiseTextEmbedder.layer_pool, embeddings.py:262):
+ * out[r, c] = sum_l weight[l] * (h[r*layers + l, c] + branch[r*layers + l, c]) + bias[0], with h
+ * FP32 [rows * layers, width], branch BF16 of the same shape or null (the last block's residual
+ * add, fused), bias null or one value; out FP32 or BF16 [rows, width]. width % 4 == 0. */
+int iris_layer_pool(const float* h, const void* branch, const float* weight, const float* bias, long rows, int layers,
+                    int width, void* out, int out_dtype, hipStream_t stream);
+
 /* F.linear on bf16 MFMA (src/iris_metal/model.py:46-52): C[m, n] = sum_k A[m, k] B[n, k] + bias[n]
  * with A BF16 [m, lda], B (the weight) BF16 [n, ldb], C in c_dtype with row stride ldc.
  * k % 64 == 0. IRIS_EPI_SILU_MUL: B holds w1 / w3 rows interleaved in 32-row groups
  * (rows 64p..64p+31 = w1 rows 32p.., rows 64p+32..64p+63 = w3 rows 32p..) and
- * C[m, j] = silu(a_j) * b_j is n/2 wide (SwiGLU, src/iris3b/nn/mlp.py:24-40). */
+ * C[m, j] = silu(a_j) * b_j is n/2 wide (SwiGLU, src/iris3b/nn/mlp.py:24-40).
+ * IRIS_EPI_SILU: C = silu(A B^T + bias) (the Linear + SiLU of the layer-wise text adapter's
+ * MLP, src/iris3b/nn/embeddings.py:131-135). */
 int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n, int k,
                    long lda, long ldb, long ldc, int epilogue, hipStream_t stream);
 
-/* Tuning hook for the benchmark sweep: force the GEMM tile (0: 256x256, 1: 256x128,
- * 2: 128x128) or restore the automatic choice (-1). No counterpart in the reference. */
+/* Tuning hook for the benchmark sweep: force the GEMM tile (an index into the tile table of
+ * gemm.hip: 0-10 eight- and four-wave tiles of 256x256, 256x192, 192x256 and 128x128; 11 the
+ * four-wave 128x128-per-wave kernel) or restore the automatic choice (-1). No counterpart in
+ * the reference. */
 int iris_gemm_force_tile(int tile);
 
 /* Up to two GEMMs of equal n, k and strides in one launch (the image and text streams of a
@@ -160,6 +194,15 @@ int iris_unpatchify_head(const void* h, const float* w, const float* bias, float
 /* s_cond = silu(t_emb + image) (src/iris_metal/model.py:207): out[r] = silu(x[r] + t[r / rows_per_batch]). */
 int iris_silu_add_rows(const float* x, const float* t, long rows, long rows_per_batch, int width, void* out,
                        int out_dtype, hipStream_t stream);
+
+/* Pre-norm residual step of the text adapter's blocks (src/iris3b/nn/embeddings.py:105-107,
+ * 139-141, 205): residual += branch (FP32 residual [rows, width], branch BF16/FP32 or null),
+ * then out = rmsnorm(residual) * weight (+ add_rows[row % add_period] when add_rows is given:
+ * the position table y_pos_embedding after the refiner's final norm, dit.py:278-279).
+ * width % 8 == 0, <= 8192; out BF16 or FP32, not aliasing residual or branch. */
+int iris_residual_rms_norm(float* residual, const void* branch, int branch_dtype, const float* weight,
+                           const float* add_rows, long add_period, long rows, int width, float eps, void* out,
+                           int out_dtype, hipStream_t stream);
 
 /* Row-block copy, dst[b*dst_batch_rows + dst_row_offset + r] = src[b*src_batch_rows + src_row_offset + r]
  * for r < rows: the [text | image] join (src/iris_metal/model.py:201-202) and the image-only

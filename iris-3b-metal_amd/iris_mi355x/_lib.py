@@ -16,7 +16,7 @@ import torch
 LIBRARY = Path(__file__).resolve().with_name("libiris_hip.so")
 
 F32, BF16 = 0, 1
-EPI_NONE, EPI_SILU_MUL = 0, 1
+EPI_NONE, EPI_SILU_MUL, EPI_SILU = 0, 1, 2
 ACT_NONE, ACT_SILU = 0, 1
 E_INVALID, E_LAUNCH, E_UNSUPPORTED = -1, -2, -3
 
@@ -35,6 +35,11 @@ _SIGNATURES: dict[str, list] = {
     "iris_gemm_bf16": [P, P, P, P, c_int, c_int, c_int, c_int, c_long, c_long, c_long, c_int, P],
     "iris_gemm_force_tile": [c_int],
     "iris_flash_attn_force_variant": [c_int],
+    "iris_flash_attn_masked": [P, P, P, c_int, c_int, c_int, c_long, c_long, c_float, P, P, c_long, c_long, P],
+    "iris_text_key_mask": [P, c_int, c_long, c_int, c_long, c_long, P, P],
+    "iris_layer_attention": [P, P, c_long, c_int, c_int, c_int, c_float, P],
+    "iris_layer_pool": [P, P, P, P, c_long, c_int, c_int, P, c_int, P],
+    "iris_residual_rms_norm": [P, P, c_int, P, P, c_long, c_long, c_int, c_float, P, c_int, P],
     "iris_gemm_bf16_grouped": [c_int, P, P, P, P, P, c_int, c_int, c_int, c_long, c_long, c_long, c_int, P],
     "iris_gemv_bf16": [P, P, c_int, c_int, c_int, P, P, c_int, P, c_int, c_int, P],
     "iris_timestep_features": [P, P, c_int, c_int, P, P],

@@ -1,5 +1,6 @@
-// Flash attention (forward, no mask) for 128-wide heads on gfx950 bf16 MFMA, with grouped
-// K/V heads and the attention gate fused into the store.
+// Flash attention (forward) for 128-wide heads on gfx950 bf16 MFMA, with grouped K/V heads and
+// the attention gate fused into the store; optionally with a per-batch key mask in which every
+// query also keeps its own position (the text refiner's `mask | eye`).
 //
 // Workgroup = 4 waves sharing one K/V head: with G = heads / kv_heads query heads per K/V
 // head, a workgroup serves hpw = min(G, 4) of them and 32 * QB * 4 / hpw query rows, one
@@ -38,6 +39,7 @@ struct AttnArgs {
   bf16* out1;
   const bf16* gate0;
   const bf16* gate1;
+  const unsigned char* key_mask;  // [batch, n_pad] 0/1 bytes, MASKED kernels only
   long ld_out, ld_gate;
   long out_brows0, out_brows1, gate_brows0, gate_brows1;
   int heads, kv_heads, n, n_pad, n_split;
@@ -96,7 +98,10 @@ __device__ __forceinline__ void store_row(const AttnArgs& p, const f32x16 (&o)[4
 // wave as global_load_lds does) -> LDS (ds_write_b128) through two LDS stages: tile t + 1 is
 // written while tile t is multiplied, tile t + 2 is loaded meanwhile. Otherwise a ring of
 // STAGES tiles filled by global_load_lds.
-template <int QB, int STAGES, int KVT, bool STAGED>
+// MASKED: query q attends key j < n iff key_mask[b, j] != 0 or j == q. A tile can then hold no
+// key of some query; its running max stays -inf and the exponentials use 0 in its place, so
+// they are exactly 0 instead of NaN.
+template <int QB, int STAGES, int KVT, bool STAGED, bool MASKED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2 : 1))) void flash_attn_kernel(
     AttnArgs p) {  // 32-row waves: two workgroups per CU (<= 256 registers per lane)
   constexpr int KB = KVT / 32;     // 32-key blocks per tile
@@ -247,7 +252,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
     }
 
     const int kv0 = t * KVT;
-    if (kv0 + KVT > p.n) {  // tail tile: keys >= n do not exist (every tile holds at least one key)
+    if constexpr (MASKED) {
+      // keys kv0 + kb*32 + 8 (r/4) + 4 g + r%4: four consecutive mask bytes per r/4
+      const unsigned char* km = p.key_mask + static_cast<long>(b) * n_pad + kv0 + 4 * g;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const unsigned int bits = *reinterpret_cast<const unsigned int*>(km + kb * 32 + 8 * r4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = kv0 + kb * 32 + 8 * r4 + 4 * g + e;
+            const bool on = key < p.n && ((bits >> (8 * e)) & 0xffu) != 0;
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+              const bool keep = on || (key < p.n && key == q0 + qb * 32 + l32);
+              if (!keep) s[kb][qb][4 * r4 + e] = -INFINITY;
+            }
+          }
+        }
+    } else if (kv0 + KVT > p.n) {  // tail tile: keys >= n do not exist (every tile holds at least one key)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -269,8 +293,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run[qb], mx * sl2);
+      // (a column with no key so far keeps m = -inf; exponents are then taken against 0)
+      const float m_use = MASKED && m_new == -INFINITY ? 0.0f : m_new;
       if (__any(m_new != m_run[qb])) {  // wave-uniform branch; alpha is 1 where the max held
-        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
         l_run[qb] *= alpha;
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
@@ -281,7 +307,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(s[kb][qb][r] * sl2 - m_new);
+          const float pv = __builtin_amdgcn_exp2f(s[kb][qb][r] * sl2 - m_use);
           s[kb][qb][r] = pv;
           sum += pv;
         }
@@ -410,6 +436,47 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
       break;
   }
   return check_launch("flash_attn");
+}
+
+extern "C" int iris_flash_attn_masked(const void* q, const void* k, const void* vt, int batch, int heads,
+                                      int kv_heads, long n, long n_pad, float scale, const void* key_mask,
+                                      void* out, long ld_out, long out_batch_rows, hipStream_t stream) {
+  IRIS_REQUIRE(batch >= 0 && heads > 0 && kv_heads > 0 && heads % kv_heads == 0,
+               "flash_attn_masked: query heads %d must be a multiple of K/V heads %d", heads, kv_heads);
+  const int group = heads / kv_heads;
+  IRIS_REQUIRE((group & (group - 1)) == 0, "flash_attn_masked: heads per K/V head must be a power of two (got %d)",
+               group);
+  IRIS_REQUIRE(n > 0 && n_pad >= n && n_pad % 64 == 0 && n_pad < (1L << 24),
+               "flash_attn_masked: n_pad must be n rounded up to a multiple of 64");
+  IRIS_REQUIRE(ld_out >= heads * 128L && ld_out % 4 == 0 && out_batch_rows >= n, "flash_attn_masked: bad output strides");
+  IRIS_REQUIRE(q && k && vt && key_mask && out, "flash_attn_masked: null pointer");
+  IRIS_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(vt, 16) && aligned(key_mask, 4) && aligned(out, 8),
+               "flash_attn_masked: misaligned pointer");
+  if (batch == 0) return IRIS_OK;
+  AttnArgs args{};
+  args.q = static_cast<const bf16*>(q);
+  args.k = static_cast<const bf16*>(k);
+  args.vt = static_cast<const bf16*>(vt);
+  args.out1 = static_cast<bf16*>(out);
+  args.key_mask = static_cast<const unsigned char*>(key_mask);
+  args.ld_out = ld_out;
+  args.out_brows1 = out_batch_rows;
+  args.heads = heads;
+  args.kv_heads = kv_heads;
+  args.n = static_cast<int>(n);
+  args.n_pad = static_cast<int>(n_pad);
+  args.n_split = 0;
+  args.hpw = group < 4 ? group : 4;
+  args.rows_per_wg = 32 * 4 / args.hpw;
+  args.n_qblocks = static_cast<int>((n + args.rows_per_wg - 1) / args.rows_per_wg);
+  args.n_hgroups = group / args.hpw;
+  const long total = static_cast<long>(batch) * kv_heads * args.n_hgroups * args.n_qblocks;
+  IRIS_REQUIRE(total < (1L << 31), "flash_attn_masked: grid too large");
+  args.total_wg = static_cast<int>(total);
+  args.scale_log2 = scale * 1.4426950408889634f;
+  // 32-key tiles: the mask logic fits in the registers of two workgroups per CU
+  flash_attn_kernel<1, 2, 32, true, true><<<dim3(args.total_wg), 256, 0, stream>>>(args);
+  return check_launch("flash_attn_masked");
 }
 
 // Tuning hook: force an attention variant (an index into kVariants) or restore the automatic

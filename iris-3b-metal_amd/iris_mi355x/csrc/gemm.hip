@@ -169,6 +169,9 @@ __device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, con
 #pragma unroll
               for (int e = 0; e < 4; ++e) v[e] += bv[e];
             }
+            if constexpr (EPI == IRIS_EPI_SILU)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = silu(v[e]);
             store_out4(crow_l + 4 * ((nl / 4) ^ sw), v[0], v[1], v[2], v[3]);
           }
         }
@@ -229,6 +232,9 @@ __device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, con
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] += bv[e];
           }
+          if constexpr (EPI == IRIS_EPI_SILU)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = silu(v[e]);
           store_out4(crow + n0, v[0], v[1], v[2], v[3]);
         }
       }
@@ -643,6 +649,11 @@ int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
     } else {
       return fail(IRIS_E_UNSUPPORTED, "gemm: tile %dx%d has no SwiGLU epilogue", BM, BN);
     }
+  } else if (epilogue == IRIS_EPI_SILU) {
+    if (c_dtype == IRIS_BF16)
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, PARTS, IRIS_EPI_SILU, bf16><<<grid, block, 0, stream>>>(args);
+    else
+      gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, PARTS, IRIS_EPI_SILU, float><<<grid, block, 0, stream>>>(args);
   } else {
     if (c_dtype == IRIS_BF16)
       gemm_kernel<BM, BN, BK, STAGES, WGM, WGN, PARTS, IRIS_EPI_NONE, bf16><<<grid, block, 0, stream>>>(args);
@@ -671,6 +682,7 @@ int device_cus() {
 // workgroup, since the register allocator spills inside the K loop when their epilogue shares
 // the persistent loop with it.
 int launch_w4(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
+  if (epilogue == IRIS_EPI_SILU) return fail(IRIS_E_UNSUPPORTED, "gemm: the four-wave tile has no SiLU epilogue");
   const int cus = device_cus();
   const dim3 all(args.total_tiles);
   if (epilogue == IRIS_EPI_SILU_MUL) {
@@ -739,6 +751,7 @@ int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
   for (const Candidate& c : candidates) {
     const TileShape t = kTiles[c.tile];
     if (epilogue == IRIS_EPI_SILU_MUL && !t.swiglu()) continue;
+    if (epilogue == IRIS_EPI_SILU && t.w4) continue;
     long tiles = 0;
     for (int i = 0; i < groups; ++i) tiles += static_cast<long>((m[i] + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
     const long slots = 256L * c.per_cu;
@@ -760,7 +773,8 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
                                       int k, long lda, long ldb, long ldc, int epilogue, hipStream_t stream) {
   IRIS_REQUIRE(groups == 1 || groups == 2, "gemm: 1 or 2 groups");
   IRIS_REQUIRE(c_dtype == IRIS_F32 || c_dtype == IRIS_BF16, "gemm: unknown output dtype");
-  IRIS_REQUIRE(epilogue == IRIS_EPI_NONE || epilogue == IRIS_EPI_SILU_MUL, "gemm: unknown epilogue");
+  IRIS_REQUIRE(epilogue == IRIS_EPI_NONE || epilogue == IRIS_EPI_SILU_MUL || epilogue == IRIS_EPI_SILU,
+               "gemm: unknown epilogue");
   IRIS_REQUIRE(n > 0 && k > 0 && k % kBK == 0, "gemm: need n > 0 and k %% 64 == 0 (got n=%d k=%d)", n, k);
   IRIS_REQUIRE(n % 4 == 0, "gemm: n %% 4 == 0 required (got %d)", n);
   IRIS_REQUIRE(epilogue != IRIS_EPI_SILU_MUL || n % 64 == 0, "gemm: the SwiGLU epilogue needs n %% 64 == 0");
@@ -779,7 +793,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
     IRIS_REQUIRE(m[i] == 0 || (a[i] && b[i] && c[i]), "gemm: null pointer");
     IRIS_REQUIRE(!a[i] || (aligned(a[i], 16) && aligned(b[i], 16) && aligned(c[i], 16)),
                  "gemm: operands must be 16-byte aligned");
-    IRIS_REQUIRE(!bias || !bias[i] || epilogue == IRIS_EPI_NONE, "gemm: bias is not supported with SwiGLU");
+    IRIS_REQUIRE(!bias || !bias[i] || epilogue != IRIS_EPI_SILU_MUL, "gemm: bias is not supported with SwiGLU");
     m_total += m[i];
   }
   IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 31), "gemm: weight too large for 32-bit offsets");

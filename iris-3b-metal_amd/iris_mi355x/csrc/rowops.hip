@@ -303,6 +303,60 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const float* __restrict_
          load4(src + (b * src_batch_rows + src_row_offset + row) * width + col));
 }
 
+// residual[r] += branch[r] (when a branch is given, stored back), then
+// out[r] = rmsnorm(residual[r]) * weight (+ add_rows[r % add_period]): the pre-norm residual
+// step of the text adapter's blocks, fused with the next input norm, or its final norm plus
+// the position table.
+template <int NC, typename TB, typename TO>
+__global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ residual, const TB* __restrict__ branch,
+                                                            const float* __restrict__ weight,
+                                                            const float* __restrict__ add_rows, long add_period,
+                                                            long rows, int width, float eps, TO* __restrict__ out) {
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int nc = width >> 3;
+  float* res = residual + row * width;
+  float x[NC][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc) {
+      load8(res + 8 * j, x[i]);
+      if (branch) {
+        float v[8];
+        load8(branch + row * width + 8 * j, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[i][e] += v[e];
+        store8(res + 8 * j, x[i]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
+    }
+  }
+  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
+  TO* o = out + row * width;
+  const float* add = add_rows ? add_rows + (row % add_period) * width : nullptr;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc) {
+      float w[8], y[8];
+      load8(weight + 8 * j, w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (x[i][e] * r) * w[e];
+      if (add) {
+        float a[8];
+        load8(add + 8 * j, a);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] += a[e];
+      }
+      store8(o + 8 * j, y);
+    }
+  }
+}
+
 int nc_bucket(int width) {
   const int need = (width / 8 + kWave - 1) / kWave;
   if (need <= 1) return 1;
@@ -496,4 +550,38 @@ extern "C" int iris_copy_rows(const float* src, float* dst, int batch, long rows
   copy_rows_kernel<<<grid, 256, 0, stream>>>(src, dst, rows, width, src_batch_rows, src_row_offset, dst_batch_rows,
                                              dst_row_offset);
   return check_launch("copy_rows");
+}
+
+extern "C" int iris_residual_rms_norm(float* residual, const void* branch, int branch_dtype, const float* weight,
+                                      const float* add_rows, long add_period, long rows, int width, float eps,
+                                      void* out, int out_dtype, hipStream_t stream) {
+  IRIS_REQUIRE(valid_dtype(branch_dtype) && valid_dtype(out_dtype), "residual_rms_norm: unknown dtype");
+  IRIS_REQUIRE(width > 0 && width % 8 == 0 && width <= 8192, "residual_rms_norm: width %% 8 == 0 and <= 8192 (got %d)",
+               width);
+  IRIS_REQUIRE(rows >= 0 && (!add_rows || add_period > 0), "residual_rms_norm: bad row counts");
+  IRIS_REQUIRE(residual && weight && out, "residual_rms_norm: null pointer");
+  IRIS_REQUIRE(aligned(residual, 16) && aligned(weight, 16) && aligned(out, 16) && (!branch || aligned(branch, 16)) &&
+                   (!add_rows || aligned(add_rows, 16)),
+               "residual_rms_norm: rows must be 16-byte aligned");
+  IRIS_REQUIRE(out != residual && (!branch || (branch != residual && branch != out)),
+               "residual_rms_norm: out and branch must not alias the residual");
+  if (rows == 0) return IRIS_OK;
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  IRIS_NC_DISPATCH(nc_bucket(width), {
+    if (branch_dtype == IRIS_BF16 && out_dtype == IRIS_BF16)
+      residual_norm_kernel<NC, bf16, bf16><<<grid, 256, 0, stream>>>(residual, (const bf16*)branch, weight, add_rows,
+                                                                     add_period, rows, width, eps, (bf16*)out);
+    else if (branch_dtype == IRIS_BF16)
+      residual_norm_kernel<NC, bf16, float><<<grid, 256, 0, stream>>>(residual, (const bf16*)branch, weight, add_rows,
+                                                                      add_period, rows, width, eps, (float*)out);
+    else if (out_dtype == IRIS_BF16)
+      residual_norm_kernel<NC, float, bf16><<<grid, 256, 0, stream>>>(residual, (const float*)branch, weight,
+                                                                      add_rows, add_period, rows, width, eps,
+                                                                      (bf16*)out);
+    else
+      residual_norm_kernel<NC, float, float><<<grid, 256, 0, stream>>>(residual, (const float*)branch, weight,
+                                                                       add_rows, add_period, rows, width, eps,
+                                                                       (float*)out);
+  })
+  return check_launch("residual_rms_norm");
 }

@@ -197,6 +197,54 @@ class HipIris:
         self.t_freqs = tables.timestep_freqs(256, cfg.timestep_max_period, self.device)
         if "t_embedder.mlp.0.weight" in sd and sd["t_embedder.mlp.0.weight"].shape[1] != 256:
             raise ValueError("HipIris expects 256 timestep frequencies")
+        self._prepare_text(sd, f32, w, swiglu)
+
+    def _prepare_text(self, sd, f32, w, swiglu) -> None:
+        """Weights of the masked text adapter (src/iris3b/nn/embeddings.py:110-266): the
+        layer-wise blocks (``lap_blocks2`` only) with their MLP hidden width zero-padded to a
+        multiple of 64 (padded columns are silu(0) = 0 and meet zero weights), the pool, the
+        refiner, and the position table."""
+        cfg, dev = self.cfg, self.device
+        self.text_layer_blocks = []
+        if cfg.text_adapter == "lap_blocks2":
+            hidden = int(cfg.text_dim * cfg.text_lap_mlp_ratio)
+            self.text_lap_hidden = _round_up(hidden, 64)
+            for i in range(2):
+                b = f"y_embedder.layer_blocks.{i}"
+                m0 = sd[f"{b}.mlp.0.weight"].detach().float()
+                m0b = sd[f"{b}.mlp.0.bias"].detach().float()
+                m2 = sd[f"{b}.mlp.2.weight"].detach().float()
+                pad = self.text_lap_hidden - hidden
+                self.text_layer_blocks.append({
+                    "norm1": f32(f"{b}.norm1.weight"), "norm2": f32(f"{b}.norm2.weight"),
+                    "qkv_w": w(f"{b}.attn.qkv"),
+                    "qkv_b": f32(f"{b}.attn.qkv.bias") if f"{b}.attn.qkv.bias" in sd else None,
+                    "proj_w": w(f"{b}.attn.proj"), "proj_b": f32(f"{b}.attn.proj.bias"),
+                    "mlp0_w": torch.nn.functional.pad(m0, (0, 0, 0, pad)).to(dev, torch.bfloat16).contiguous(),
+                    "mlp0_b": torch.nn.functional.pad(m0b, (0, pad)).to(dev).contiguous(),
+                    "mlp2_w": torch.nn.functional.pad(m2, (0, pad)).to(dev, torch.bfloat16).contiguous(),
+                    "mlp2_b": f32(f"{b}.mlp.2.bias"),
+                })
+            self.text_pool_w = f32("y_embedder.layer_pool.weight")
+            self.text_pool_b = f32("y_embedder.layer_pool.bias")
+            refiner = "y_embedder.refiner"
+        else:
+            refiner = "y_embedder"
+        self.text_one = torch.ones(1, device=dev)  # a one-layer pool: the FP32 -> BF16 cast of blocks2 input
+        self.text_proj_w, self.text_proj_b = w(f"{refiner}.proj"), f32(f"{refiner}.proj.bias")
+        self.text_blocks = []
+        for i in range(2):
+            b = f"{refiner}.blocks.{i}"
+            blk = {"norm1": f32(f"{b}.norm1.weight"), "norm2": f32(f"{b}.norm2.weight"),
+                   "qkv_w": w(f"{b}.attn.qkv"),
+                   "qkv_b": f32(f"{b}.attn.qkv.bias") if f"{b}.attn.qkv.bias" in sd else None,
+                   "q_norm": f32(f"{b}.attn.q_norm.weight"), "k_norm": f32(f"{b}.attn.k_norm.weight"),
+                   "proj_w": w(f"{b}.attn.proj"), "proj_b": f32(f"{b}.attn.proj.bias")}
+            blk["w13"], blk["w2"] = swiglu(f"{b}.mlp")
+            self.text_blocks.append(blk)
+        self.text_norm = f32(f"{refiner}.norm.weight")
+        self.text_pos = f32("y_pos_embedding").reshape(-1, cfg.hidden_size)
+        self._text_ws: dict | None = None
 
     # -- per-shape state ----------------------------------------------------------------
     def _workspace(self, shape: _Shape) -> dict:
@@ -478,13 +526,126 @@ class HipIris:
         return HipIrisDiT(self)
 
     # -- conditioning -------------------------------------------------------------------
-    def encode_text(self, states: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-        """Encoder states ``[B, T, layers, dim]`` -> trunk text tokens (src/iris_metal/model.py:133-145).
+    def _text_workspace(self, batch: int, n: int) -> dict:
+        if self._text_ws is not None and self._text_ws["key"] == (batch, n):
+            return self._text_ws
+        cfg, dev = self.cfg, self.device
+        D, H, td = cfg.hidden_size, cfg.num_heads, cfg.text_dim
+        n_pad = _round_up(n, 64)
+        rows = batch * n
+        bf16, f32 = torch.bfloat16, torch.float32
 
-        The layer-attentive text adapter runs once per prompt and is not part of the denoise
-        step; it is not implemented on the GPU yet, so callers pass prepared tokens."""
-        raise NotImplementedError("HipIris.encode_text: the text adapter is not on the HIP path yet; "
-                                  "pass prepared text tokens [B, T, D] to __call__")
+        def e(*s, dtype=bf16):
+            return torch.empty(*s, device=dev, dtype=dtype)
+
+        ws = {
+            "key": (batch, n), "n_pad": n_pad,
+            "Y": e(rows, D, dtype=f32), "hy": e(rows, D), "qkv": e(rows, 3 * D), "att": e(rows, D),
+            "br": e(rows, D), "hh": e(rows, self.hidden_pad), "pooled": e(rows, td),
+            "q": e(batch, H, n_pad, HEAD_DIM), "k": e(batch, H, n_pad, HEAD_DIM),
+            # V^T columns of tokens >= n must stay zero: v_heads_t never writes them
+            "vt": torch.zeros(batch, H, HEAD_DIM, n_pad, device=dev, dtype=bf16),
+            "kmask": e(batch, n_pad, dtype=torch.uint8),
+            # the refiner has no RoPE: the fused QK-norm kernel runs with the identity rotation
+            "cos": torch.ones(n_pad, HEAD_DIM // 2, device=dev), "sin": torch.zeros(n_pad, HEAD_DIM // 2, device=dev),
+        }
+        if cfg.text_adapter == "lap_blocks2":
+            L = cfg.text_lap_num_layers
+            r = rows * L
+            ws.update({"H": e(r, td, dtype=f32), "hn": e(r, td), "lqkv": e(r, 3 * td), "latt": e(r, td),
+                       "lbr": e(r, td), "lmh": e(r, self.text_lap_hidden)})
+        else:
+            ws["flat"] = e(rows, td, dtype=f32)
+        self._text_ws = ws
+        return ws
+
+    @torch.no_grad()
+    def encode_text(self, states: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        """Encoder states -> trunk text tokens ``[B, T, D]`` FP32 (src/iris_metal/model.py:133-145),
+        ``T = min(len, text_len)``: the masked text adapter (src/iris3b/nn/embeddings.py:143-266)
+        plus the position table (src/iris3b/models/dit.py:263-281), once per prompt.
+
+        ``states``: ``[B, T_in, layers, text_dim]`` for ``lap_blocks2``, ``[B, T_in, text_dim]`` for
+        ``blocks2``; ``mask``: the encoder's ``[B, T_in]`` attention mask (1 = real token).
+        BF16 GEMM operands with FP32 accumulation, FP32 residuals, norms and softmax."""
+        cfg, eps, dev = self.cfg, self.eps, self.device
+        D, H, td = cfg.hidden_size, cfg.num_heads, cfg.text_dim
+        if mask is None:
+            raise ValueError(f"text_adapter={cfg.text_adapter!r} requires the encoder's [B, T] attention mask")
+        n = min(states.shape[1], cfg.text_len)
+        lap = cfg.text_adapter == "lap_blocks2"
+        if mask.dim() != 2:
+            raise ValueError(f"text mask must be [B, T], got {tuple(mask.shape)}")
+        if lap:
+            expected = (mask.shape[0], min(mask.shape[1], cfg.text_len), cfg.text_lap_num_layers, td)
+            got = (states.shape[0], n, *states.shape[2:])
+            if states.dim() != 4 or got != expected:
+                raise ValueError(f"layerwise text states must be {expected}, got {got}")
+            L, lheads = cfg.text_lap_num_layers, cfg.text_lap_num_heads
+            if L > 16 or td % lheads or td // lheads > 128:
+                raise ValueError("HipIris.encode_text: at most 16 encoder layers and heads of at most 128 values")
+        else:
+            got = (states.shape[0], n)
+            if states.dim() != 3 or states.shape[2] != td or got != (mask.shape[0], min(mask.shape[1], cfg.text_len)):
+                raise ValueError(f"text states must be [B, T, {td}] with a matching [B, T] mask, got "
+                                 f"{tuple(states.shape)} and {tuple(mask.shape)}")
+        B = states.shape[0]
+        if B == 0 or n == 0:
+            return torch.empty(B, n, D, device=dev, dtype=torch.float32)
+        ws = self._text_workspace(B, n)
+        states = states.to(dev, torch.float32).contiguous()
+        mask = mask.to(dev)
+        if mask.dtype not in K._MASK_KINDS:
+            mask = mask.to(torch.float32)
+        if mask.stride(1) != 1:
+            mask = mask.contiguous()
+        K.text_key_mask(mask, n, ws["kmask"])
+        rows = B * n
+        Y = ws["Y"]
+
+        if lap:
+            # per-token attention over encoder layers, two pre-norm blocks, then the learned pool
+            H_, hn, qkv, att, br, mh = (ws[k] for k in ("H", "hn", "lqkv", "latt", "lbr", "lmh"))
+            T_in = states.shape[1]
+            K.copy_rows(states.view(B * T_in * L, td), H_, B, n * L, 0, T_in * L, 0, n * L)
+            K.residual_rms_norm(H_, None, self.text_layer_blocks[0]["norm1"], eps, hn)
+            for i, blk in enumerate(self.text_layer_blocks):
+                K.linear(hn, blk["qkv_w"], blk["qkv_b"], out=qkv)
+                K.layer_attention(qkv, att, L, lheads)
+                K.linear(att, blk["proj_w"], blk["proj_b"], out=br)
+                K.residual_rms_norm(H_, br, blk["norm2"], eps, hn)
+                K.linear(hn, blk["mlp0_w"], blk["mlp0_b"], out=mh, silu=True)
+                K.linear(mh, blk["mlp2_w"], blk["mlp2_b"], out=br)
+                if i + 1 < len(self.text_layer_blocks):
+                    K.residual_rms_norm(H_, br, self.text_layer_blocks[i + 1]["norm1"], eps, hn)
+            K.layer_pool(H_, br, self.text_pool_w, self.text_pool_b, L, ws["pooled"])
+        else:
+            T_in = states.shape[1]
+            K.copy_rows(states.view(B * T_in, td), ws["flat"], B, n, 0, T_in, 0, n)
+            K.layer_pool(ws["flat"], None, self.text_one, None, 1, ws["pooled"])  # FP32 -> BF16
+
+        # refiner: Linear, two masked pre-norm blocks, RMSNorm, + position table
+        K.linear(ws["pooled"], self.text_proj_w, self.text_proj_b, out=Y)
+        hy, qkv, att, br, hh = ws["hy"], ws["qkv"], ws["att"], ws["br"], ws["hh"]
+        q, k, vt, cos, sin = ws["q"], ws["k"], ws["vt"], ws["cos"], ws["sin"]
+        out = torch.empty(B, n, D, device=dev, dtype=torch.float32)
+        K.residual_rms_norm(Y, None, self.text_blocks[0]["norm1"], eps, hy)
+        for i, blk in enumerate(self.text_blocks):
+            K.linear(hy, blk["qkv_w"], blk["qkv_b"], out=qkv)
+            pv = qkv.view(B, n, 3 * D)
+            K.qk_norm_rope(pv, blk["q_norm"], cos, sin, eps, H, 0, out=q)
+            K.qk_norm_rope(pv, blk["k_norm"], cos, sin, eps, H, D, out=k)
+            K.v_heads_t(pv, H, vt, 2 * D, 0)
+            K.flash_attention_masked(q, k, vt, n, ws["kmask"], att)
+            K.linear(att, blk["proj_w"], blk["proj_b"], out=br)
+            K.residual_rms_norm(Y, br, blk["norm2"], eps, hy)
+            K.linear(hy, blk["w13"], out=hh, swiglu=True)
+            K.linear(hh, blk["w2"], out=br)
+            if i + 1 < len(self.text_blocks):
+                K.residual_rms_norm(Y, br, self.text_blocks[i + 1]["norm1"], eps, hy)
+            else:
+                K.residual_rms_norm(Y, br, self.text_norm, eps, out.view(rows, D), add_rows=self.text_pos[:n])
+        return out
 
 
 class HipIrisDiT:

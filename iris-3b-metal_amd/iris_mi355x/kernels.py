@@ -272,12 +272,15 @@ def linear(
     out: torch.Tensor | None = None,
     out_dtype: torch.dtype = torch.bfloat16,
     swiglu: bool = False,
+    silu: bool = False,
 ) -> torch.Tensor:
     """``F.linear(x, weight, bias)`` on the MFMA GEMM; BF16 operands, FP32 accumulation.
 
     ``x``: BF16 ``[..., K]`` with contiguous rows; ``weight``: BF16 ``[N, K]``; ``bias``: FP32
     ``[N]``. With ``swiglu`` the weight is a ``pack_swiglu`` pair and the result is
-    ``silu(x w1^T) * (x w3^T)``, N/2 wide. K must be a multiple of 64."""
+    ``silu(x w1^T) * (x w3^T)``, N/2 wide; with ``silu`` the result is ``silu(x w^T + bias)``.
+    K must be a multiple of 64."""
+    _require(not (swiglu and silu), "linear: choose one epilogue")
     _on_gpu(x, weight, bias, out)
     _require(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, "linear takes BF16 operands")
     _require(x.stride(-1) == 1 and weight.is_contiguous(), "linear needs row-contiguous operands")
@@ -296,7 +299,8 @@ def linear(
     out2 = out.reshape(-1, n_out)
     L.call(
         "iris_gemm_bf16", L.ptr(x2), L.ptr(weight), L.ptr(bias), L.ptr(out2), L.dtype_code(out.dtype), m, n, k,
-        x2.stride(0), weight.stride(0), out2.stride(0), L.EPI_SILU_MUL if swiglu else L.EPI_NONE, L.stream(),
+        x2.stride(0), weight.stride(0), out2.stride(0),
+        L.EPI_SILU_MUL if swiglu else (L.EPI_SILU if silu else L.EPI_NONE), L.stream(),
     )
     return out
 
@@ -378,6 +382,112 @@ def flash_attention(
         L.ptr(out0), L.ptr(out1), ld_out, ob[0], ob[1], L.ptr(gate0), L.ptr(gate1), ld_gate, gb[0], gb[1],
         L.stream(),
     )
+
+
+def flash_attention_masked(q, k, vt, n: int, key_mask: torch.Tensor, out: torch.Tensor, scale: float | None = None):
+    """The text refiner's attention: ``flash_attention`` where query ``i`` of batch ``b`` sees key
+    ``j < n`` only if ``key_mask[b, j]`` or ``j == i`` (``mask | eye``, src/iris3b/nn/embeddings.py:199-201).
+    ``key_mask``: uint8 ``[B, N_pad]`` from ``text_key_mask``; ``out``: BF16 ``[B, rows >= n, heads*128]``
+    or ``[B*n, heads*128]`` with unit column stride."""
+    batch, heads, n_pad, hd = q.shape
+    kv_heads = k.shape[1]
+    _on_gpu(q, k, vt, key_mask, out)
+    _require(hd == HEAD_DIM and k.shape == (batch, kv_heads, n_pad, HEAD_DIM), "flash_attention_masked: bad q/k shapes")
+    _require(vt.shape == (batch, kv_heads, HEAD_DIM, n_pad), "flash_attention_masked: bad vt shape")
+    _require(all(t.dtype == torch.bfloat16 and t.is_contiguous() for t in (q, k, vt)),
+             "flash_attention_masked: BF16 inputs")
+    _require(key_mask.dtype == torch.uint8 and key_mask.shape == (batch, n_pad) and key_mask.is_contiguous(),
+             f"flash_attention_masked: key_mask must be uint8 [{batch}, {n_pad}]")
+    _require(out.dtype == torch.bfloat16 and out.stride(-1) == 1 and out.shape[-1] == heads * HEAD_DIM,
+             "flash_attention_masked: BF16 row-major output")
+    if out.dim() == 3:
+        _require(out.shape[0] == batch and out.shape[1] >= n, "flash_attention_masked: output too small")
+        batch_rows = out.stride(0) // out.stride(1)
+        _require(out.stride(0) == batch_rows * out.stride(1), "flash_attention_masked: output batch stride")
+    else:
+        _require(out.shape[0] >= batch * n, "flash_attention_masked: output too small")
+        batch_rows = n
+    scale = HEAD_DIM ** -0.5 if scale is None else scale
+    L.call("iris_flash_attn_masked", L.ptr(q), L.ptr(k), L.ptr(vt), batch, heads, kv_heads, n, n_pad, float(scale),
+           L.ptr(key_mask), L.ptr(out), out.stride(-2), batch_rows, L.stream())
+    return out
+
+
+_MASK_KINDS = {torch.bool: 0, torch.uint8: 0, torch.int8: 0, torch.int32: 1, torch.float32: 2, torch.int64: 3}
+
+
+def text_key_mask(mask: torch.Tensor, n: int, out: torch.Tensor) -> torch.Tensor:
+    """``mask[:, :n].bool()`` as the zero-padded uint8 ``[B, N_pad]`` key mask of ``flash_attention_masked``."""
+    _on_gpu(mask, out)
+    _require(mask.dtype in _MASK_KINDS, f"text mask dtype {mask.dtype} not supported (bool, uint8, int32, int64, float32)")
+    _require(mask.dim() == 2 and mask.stride(1) == 1 and mask.shape[1] >= n, "text mask must be [B, >= n] row-major")
+    _require(out.dtype == torch.uint8 and out.dim() == 2 and out.shape[0] == mask.shape[0] and out.is_contiguous(),
+             "text_key_mask: out must be uint8 [B, N_pad]")
+    L.call("iris_text_key_mask", L.ptr(mask), _MASK_KINDS[mask.dtype], mask.stride(0), mask.shape[0], n, out.shape[1],
+           L.ptr(out), L.stream())
+    return out
+
+
+def layer_attention(qkv: torch.Tensor, out: torch.Tensor, seq_len: int, heads: int, scale: float | None = None):
+    """Attention of each text token over its ``seq_len`` encoder-layer states (no mask, no QK norm):
+    ``qkv`` BF16 ``[S*seq_len, 3*heads*d]`` -> ``out`` BF16 ``[S*seq_len, heads*d]``
+    (src/iris3b/nn/embeddings.py:139-141, src/iris3b/nn/attention.py:117-132)."""
+    _on_gpu(qkv, out)
+    rows, width3 = qkv.shape
+    _require(qkv.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and qkv.is_contiguous() and out.is_contiguous(),
+             "layer_attention works on contiguous BF16")
+    _require(width3 % (3 * heads) == 0 and rows % seq_len == 0 and out.shape == (rows, width3 // 3),
+             "layer_attention: bad shapes")
+    d = width3 // (3 * heads)
+    scale = d ** -0.5 if scale is None else scale
+    L.call("iris_layer_attention", L.ptr(qkv), L.ptr(out), rows // seq_len, seq_len, heads, d, float(scale), L.stream())
+    return out
+
+
+def layer_pool(h: torch.Tensor, branch: torch.Tensor | None, weight: torch.Tensor, bias: torch.Tensor | None,
+               layers: int, out: torch.Tensor) -> torch.Tensor:
+    """``layer_pool((h + branch).transpose(1, 2)).squeeze(-1)`` over ``[R, layers, W]`` states
+    (src/iris3b/nn/embeddings.py:262); ``h`` FP32, ``branch`` BF16 or None, ``out`` ``[R, W]``."""
+    _on_gpu(h, branch, weight, bias, out)
+    _require_fp32(h=h, weight=weight)
+    width = h.shape[-1]
+    rows = h.numel() // (layers * width)
+    _require(h.is_contiguous() and h.numel() == rows * layers * width, "layer_pool: bad states")
+    if branch is not None:
+        _require(branch.dtype == torch.bfloat16 and branch.is_contiguous() and branch.numel() == h.numel(),
+                 "layer_pool: branch must be BF16 like h")
+    if bias is not None:
+        _require_fp32(bias=bias)
+    _require(weight.numel() == layers and (bias is None or bias.numel() == 1), "layer_pool: weight is [1, layers]")
+    _require(out.is_contiguous() and out.numel() == rows * width, "layer_pool: bad out")
+    L.call("iris_layer_pool", L.ptr(h), L.ptr(branch), L.ptr(weight), L.ptr(bias), rows, layers, width, L.ptr(out),
+           L.dtype_code(out.dtype), L.stream())
+    return out
+
+
+def residual_rms_norm(residual: torch.Tensor, branch: torch.Tensor | None, weight: torch.Tensor, eps: float,
+                      out: torch.Tensor, add_rows: torch.Tensor | None = None) -> torch.Tensor:
+    """``residual += branch`` (in place, FP32), then ``out = rmsnorm(residual) * weight (+ add_rows)``
+    (the pre-norm residual of src/iris3b/nn/embeddings.py:105-107, 139-141; ``add_rows``
+    ``[P, W]`` is added to row ``r`` as ``add_rows[r % P]``)."""
+    _on_gpu(residual, branch, weight, out, add_rows)
+    _require_fp32(residual=residual, weight=weight)
+    width = residual.shape[-1]
+    rows = residual.numel() // width
+    _require(residual.is_contiguous() and out.is_contiguous() and out.numel() == residual.numel(),
+             "residual_rms_norm: contiguous residual and out of one shape")
+    if branch is not None:
+        _require(branch.is_contiguous() and branch.numel() == residual.numel(), "residual_rms_norm: bad branch")
+    period = 0
+    if add_rows is not None:
+        _require_fp32(add_rows=add_rows)
+        _require(add_rows.is_contiguous() and add_rows.shape[-1] == width, "residual_rms_norm: bad add_rows")
+        period = add_rows.numel() // width
+    _require(weight.numel() == width, "residual_rms_norm: weight width")
+    L.call("iris_residual_rms_norm", L.ptr(residual), L.ptr(branch),
+           L.dtype_code(branch.dtype) if branch is not None else L.F32, L.ptr(weight), L.ptr(add_rows), period, rows,
+           width, float(eps), L.ptr(out), L.dtype_code(out.dtype), L.stream())
+    return out
 
 
 def gemv(

@@ -93,8 +93,54 @@ def test_upstream_dit_surface_matches_engine(released):
     text = torch.randn(1, cfg.text_len, cfg.hidden_size, generator=g).to(DEV)
     out = engine.as_dit()(x, t, None, y_mask=None, prepared_text=text, precompute_modulation=True)
     assert torch.equal(out.x, engine(x, t, text))
-    with pytest.raises(NotImplementedError):
-        engine.as_dit()(x, t, torch.zeros(1, 16, 3, 64, device=DEV), y_mask=torch.ones(1, 16, device=DEV))
+    # without prepared text the encoder states go through the adapter first (dit.py:283-315)
+    states = torch.randn(1, 16, cfg.text_lap_num_layers, cfg.text_dim, generator=g).to(DEV)
+    mask = torch.ones(1, 16, device=DEV, dtype=torch.int64)
+    out = engine.as_dit()(x, t, states, y_mask=mask)
+    assert torch.equal(out.x, engine(x, t, engine.encode_text(states, mask)))
+    with pytest.raises(ValueError, match="mask"):
+        engine.as_dit()(x, t, states, y_mask=None)
+
+
+def _prompt_mask(batch, n_in, lengths):
+    mask = torch.zeros(batch, n_in, dtype=torch.int64)
+    for b, n in enumerate(lengths):
+        mask[b, :n] = 1
+    return mask
+
+
+def test_released_encode_text_matches_oracle(released):
+    """The layer-wise adapter, refiner and position table: prompts of 11 and 16 real tokens and an
+    all-pad prompt, encoder states longer than text_len (truncated as the reference does)."""
+    cfg, sd, engine = released
+    g = torch.Generator().manual_seed(6)
+    n_in = cfg.text_len + 3
+    states = torch.randn(3, n_in, cfg.text_lap_num_layers, cfg.text_dim, generator=g)
+    mask = _prompt_mask(3, n_in, (11, n_in, 0))
+    want = O.embed_text(sd, cfg, states, mask)
+    sd_, md_ = states.to(DEV), mask.to(DEV)
+    got = engine.encode_text(sd_, md_)
+    assert got.shape == (3, cfg.text_len, cfg.hidden_size) and got.dtype == torch.float32
+    check(got, want, "released encode_text")
+    for b in range(3):
+        check(got[b], want[b], f"released encode_text prompt {b}")
+    assert torch.equal(sd_.cpu(), states) and torch.equal(md_.cpu(), mask)  # inputs untouched
+    assert torch.equal(engine.encode_text(sd_, md_.bool()), got)  # any mask dtype, same result
+    with pytest.raises(ValueError, match="layerwise text states"):
+        engine.encode_text(sd_[:, :, :2], md_)
+
+
+def test_blocks2_text_adapter_matches_oracle():
+    """The refiner-only adapter (text_adapter='blocks2') on [B, T, text_dim] states."""
+    from dataclasses import replace
+
+    cfg = replace(RELEASED_TOPOLOGY, text_adapter="blocks2")
+    sd = synthetic_state_dict(cfg, seed=3)
+    engine = HipIris(cfg, sd, device=DEV)
+    g = torch.Generator().manual_seed(7)
+    states = torch.randn(2, cfg.text_len, cfg.text_dim, generator=g)
+    mask = _prompt_mask(2, cfg.text_len, (5, 16))
+    check(engine.encode_text(states.to(DEV), mask.to(DEV)), O.embed_text(sd, cfg, states, mask), "blocks2 encode_text")
 
 
 def test_unsupported_topology_is_rejected():
@@ -127,6 +173,21 @@ def test_iris3b_shallow_forward_at_256px_matches_oracle(iris3b_blocks):
     engine = HipIris(cfg, sd, device=DEV)
     got = engine(x.to(DEV), t.to(DEV), text.to(DEV))
     check(got, want, "iris3b shallow 256px")
+
+
+def test_iris3b_encode_text_matches_oracle(iris3b_blocks):
+    """Full-width adapter: 12 encoder layers of 2560 (32 heads of 80), MLP 3328, refiner of 20
+    heads of 128 with SwiGLU 6826, 300 text tokens of which 123 are real."""
+    cfg, sd = iris3b_blocks
+    g = torch.Generator().manual_seed(8)
+    states = torch.randn(1, cfg.text_len, cfg.text_lap_num_layers, cfg.text_dim, generator=g)
+    mask = _prompt_mask(1, cfg.text_len, (123,))
+    torch.set_num_threads(max(1, torch.get_num_threads()))
+    want = O.embed_text(sd, cfg, states, mask)
+    engine = HipIris(cfg, sd, device=DEV)
+    got = engine.encode_text(states.to(DEV), mask.to(DEV))
+    check(got, want, "iris3b encode_text")
+    check(got[:, :123], want[:, :123], "iris3b encode_text real tokens")
 
 
 def test_graph_replays_match_eager_forward(released):

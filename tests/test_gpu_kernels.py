@@ -263,6 +263,119 @@ def test_flash_attention_trunk_shape_with_gate_and_split():
         close_bf16(got[sel, hh], want, scale=1.0, floor=4e-3)
 
 
+# -- text adapter ---------------------------------------------------------------------------
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+def test_gemm_silu_epilogue(tile):
+    """Linear + SiLU of the layer-wise blocks' MLP (hidden 83 zero-padded to 128 at the released
+    width, 3328 at full width)."""
+    g = gen(21)
+    for m, n, k in ((300, 128, 64), (97, 3328, 128)):
+        a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+        w = (0.1 * torch.randn(n, k, generator=g)).to(torch.bfloat16)
+        bias = torch.randn(n, generator=g)
+        _lib.call("iris_gemm_force_tile", tile)
+        try:
+            out16 = K.linear(a.to(DEV), w.to(DEV), bias.to(DEV), silu=True)
+            out32 = K.linear(a.to(DEV), w.to(DEV), bias.to(DEV), out_dtype=torch.float32, silu=True)
+        finally:
+            _lib.call("iris_gemm_force_tile", -1)
+        want = F.silu(_gemm_ref(a, w, bias))
+        torch.testing.assert_close(out32.cpu(), want, rtol=1e-4, atol=1e-4)
+        close_bf16(out16, want)
+
+
+def test_gemm_silu_is_refused_by_the_four_wave_tile():
+    a = torch.zeros(64, 64, device=DEV, dtype=torch.bfloat16)
+    w = torch.zeros(64, 64, device=DEV, dtype=torch.bfloat16)
+    _lib.call("iris_gemm_force_tile", 11)
+    try:
+        with pytest.raises(_lib.IrisKernelError, match="SiLU"):
+            K.linear(a, w, silu=True)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+
+
+def _text_mask(b, n_in, n, seed, dtype):
+    """Batch 0: pad keys first (so early key tiles hold no key of later queries), then random real
+    tokens, then padding; batch 1: an all-pad prompt (identity attention); batch 2: all real."""
+    g = gen(seed)
+    mask = torch.zeros(b, n_in)
+    lead = min(40, n // 4)
+    mask[0, lead:int(0.8 * n)] = (torch.rand(int(0.8 * n) - lead, generator=g) < 0.7).float()
+    if b > 2:
+        mask[2] = 1.0
+    return mask.to(dtype)
+
+
+@pytest.mark.parametrize("b,h,n,mask_dtype", [(2, 2, 16, torch.int64), (1, 20, 300, torch.bool),
+                                               (3, 4, 77, torch.float32), (2, 2, 130, torch.int32)])
+def test_flash_attention_masked_text_refiner(b, h, n, mask_dtype):
+    q, k, v, qd, kd, vt = _attn_inputs(b, h, h, n, 11)
+    n_pad = qd.shape[2]
+    mask = _text_mask(b, n + 5, n, 12, mask_dtype)
+    keep = mask[:, :n].bool()[:, None, None, :] | torch.eye(n, dtype=torch.bool)
+    want = O.attention(q.float(), k.float(), v.float(), keep).transpose(1, 2).reshape(b, n, h * 128)
+    km = torch.full((b, n_pad), 9, device=DEV, dtype=torch.uint8)
+    K.text_key_mask(mask.to(DEV), n, km)
+    want_km = torch.zeros(b, n_pad, dtype=torch.uint8)
+    want_km[:, :n] = mask[:, :n].bool().to(torch.uint8)
+    assert torch.equal(km.cpu(), want_km)
+    out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+    K.flash_attention_masked(qd, kd, vt, n, km, out)
+    got = out.view(b, n, -1)
+    assert torch.isfinite(got.float()).all()
+    close_bf16(got, want, scale=1.0, floor=4e-3)
+    if b > 1:  # the all-pad prompt attends only to itself: out = v, to BF16 rounding
+        torch.testing.assert_close(got[1].float().cpu(), v[1].transpose(0, 1).reshape(n, h * 128).float())
+
+
+@pytest.mark.parametrize("seqs,L,heads,d", [(37, 12, 32, 80), (50, 3, 4, 16), (5, 16, 1, 128)])
+def test_layer_attention_matches_sdpa(seqs, L, heads, d):
+    g = gen(13)
+    qkv = torch.randn(seqs * L, 3 * heads * d, generator=g).to(torch.bfloat16)
+    q, k, v = (t.transpose(1, 2) for t in qkv.float().view(seqs, L, 3, heads, d).unbind(2))
+    want = O.attention(q, k, v).transpose(1, 2).reshape(seqs * L, heads * d)
+    out = torch.zeros(seqs * L, heads * d, device=DEV, dtype=torch.bfloat16)
+    K.layer_attention(qkv.to(DEV), out, L, heads)
+    close_bf16(out, want)
+
+
+@pytest.mark.parametrize("width", [64, 2560])
+def test_layer_pool_with_fused_residual(width):
+    rows, L = 45, 12
+    g = gen(14)
+    h = torch.randn(rows * L, width, generator=g)
+    br = torch.randn(rows * L, width, generator=g).to(torch.bfloat16)
+    w, b = 0.3 * torch.randn(1, L, generator=g), torch.randn(1, generator=g)
+    want = F.linear((h + br.float()).view(rows, L, width).transpose(1, 2), w, b).squeeze(-1)
+    out = torch.empty(rows, width, device=DEV)
+    K.layer_pool(h.to(DEV), br.to(DEV), w.to(DEV), b.to(DEV), L, out)
+    torch.testing.assert_close(out.cpu(), want, rtol=1e-5, atol=1e-5)
+    out16 = torch.empty(rows, width, device=DEV, dtype=torch.bfloat16)
+    K.layer_pool(h[:rows].to(DEV), None, torch.ones(1, device=DEV), None, 1, out16)
+    assert torch.equal(out16.cpu(), h[:rows].to(torch.bfloat16))  # one layer, weight 1: the BF16 cast
+
+
+@pytest.mark.parametrize("branch_dtype", [None, torch.bfloat16, torch.float32])
+def test_residual_rms_norm_with_position_rows(branch_dtype):
+    b, n, width = 2, 300, 2560
+    g = gen(15)
+    res = torch.randn(b * n, width, generator=g)
+    br = None if branch_dtype is None else torch.randn(b * n, width, generator=g).to(branch_dtype)
+    w = 1 + 0.02 * torch.randn(width, generator=g)
+    pos = torch.randn(n, width, generator=g)
+    want_res = res if br is None else res + br.float()
+    want = O.rms_norm(want_res, w, 1e-6)
+    r = res.to(DEV)
+    out = torch.empty(b * n, width, device=DEV)
+    K.residual_rms_norm(r, None if br is None else br.to(DEV), w.to(DEV), 1e-6, out, add_rows=pos.to(DEV))
+    assert torch.equal(r.cpu(), want_res)  # one FP32 add, as torch does it
+    torch.testing.assert_close(out.cpu(), want + pos.repeat(b, 1), rtol=2e-5, atol=2e-5)
+    out16 = torch.empty(b * n, width, device=DEV, dtype=torch.bfloat16)
+    K.residual_rms_norm(r, None, w.to(DEV), 1e-6, out16)
+    close_bf16(out16, want)
+
+
 # -- conditioning, pixel stage, sampler ----------------------------------------------------
 def test_gemv_with_core_biases():
     n, k, j, b = 1536, 256, 3, 2
