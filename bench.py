@@ -14,7 +14,10 @@ Prints one JSON line. Besides the driver's fields it carries:
 - ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included);
 - ``graph_ms_per_step``: the same step with the forward replayed from its recorded HIP graph.
   The timed region itself launches eagerly, so that every GEMM launch can be bracketed by
-  events.
+  events;
+- ``encode_text``: the once-per-prompt text adapter (12 encoder layers of 2560 per token,
+  300 tokens of which 200 are real, batch 1) on the GPU, and the FP32 CPU oracle of the same
+  prompt beside it (unless ``--no-cpu-baseline``).
 """
 
 from __future__ import annotations
@@ -95,12 +98,12 @@ class LaunchTimer:
         orig_linear, orig_grouped = K.linear, K.linear_grouped
         timer = self
 
-        def linear(x, weight, bias=None, out=None, out_dtype=torch.bfloat16, swiglu=False):
+        def linear(x, weight, bias=None, out=None, out_dtype=torch.bfloat16, swiglu=False, silu=False):
             if not timer.enabled:
-                return orig_linear(x, weight, bias, out, out_dtype, swiglu)
+                return orig_linear(x, weight, bias, out, out_dtype, swiglu, silu)
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
-            res = orig_linear(x, weight, bias, out, out_dtype, swiglu)
+            res = orig_linear(x, weight, bias, out, out_dtype, swiglu, silu)
             e.record()
             m = x.numel() // x.shape[-1]
             k = x.shape[-1] if x.shape[-1] != timer.patch_k else 3 * timer.cfg.patch_size ** 2
@@ -178,6 +181,34 @@ def cpu_baseline(height: int, width: int, n_text: int, seed: int = 0) -> dict:
     }
 
 
+def text_prompt(cfg, real: int = 200, seed: int = 2):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    states = torch.randn(1, cfg.text_len, cfg.text_lap_num_layers, cfg.text_dim, generator=g)
+    mask = torch.zeros(1, cfg.text_len, dtype=torch.int64)
+    mask[0, :real] = 1
+    return states, mask
+
+
+def cpu_encode_text(cfg, text_sd: dict) -> dict:
+    """The FP32 CPU oracle of the text adapter on the prompt ``text_prompt`` draws, median of 3."""
+    import torch
+
+    from oracle import iris_oracle as O
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    states, mask = text_prompt(cfg)
+    runs = []
+    with torch.no_grad():
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.embed_text(text_sd, cfg, states, mask)
+            runs.append(time.perf_counter() - t0)
+    return {"ms_per_prompt": 1000.0 * sorted(runs)[1], "cores": threads, "kind": "port"}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -210,6 +241,9 @@ def main() -> None:
     sd = synthetic_state_dict(cfg, seed=0, device=dev)
     engine = HipIris(cfg, sd, device=dev)
     engine.graphs = False  # eager launches in the timed region (GEMM events); graphs timed after
+    text_sd = None
+    if not args.no_cpu_baseline:  # the adapter's weights, for its CPU oracle
+        text_sd = {k: v.cpu() for k, v in sd.items() if k.startswith(("y_embedder.", "y_pos_embedding"))}
     del sd
     torch.cuda.empty_cache()
 
@@ -270,8 +304,26 @@ def main() -> None:
         torch.cuda.synchronize()
         turbo_s = time.perf_counter() - t0
 
+    # the once-per-prompt text adapter
+    states, mask = text_prompt(cfg)
+    states_d, mask_d = states.to(dev), mask.to(dev)
+    engine.encode_text(states_d, mask_d)
+    torch.cuda.synchronize()
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        engine.encode_text(states_d, mask_d)
+    torch.cuda.synchronize()
+    encode = {"ms_per_prompt": 1000.0 * (time.perf_counter() - t0) / reps, "batch": 1, "tokens": cfg.text_len,
+              "real_tokens": int(mask.sum()), "encoder_layers": cfg.text_lap_num_layers, "text_dim": cfg.text_dim,
+              "cpu_oracle": None}
+    del states_d, mask_d
+
     cpu = None
     if not args.no_cpu_baseline:
+        print("[bench] CPU oracle of the text adapter", file=sys.stderr, flush=True)
+        encode["cpu_oracle"] = cpu_encode_text(cfg, text_sd)
+        del text_sd
         print("[bench] CPU baseline (oracle, one block of each kind)", file=sys.stderr, flush=True)
         cpu = cpu_baseline(size, size, n_text)
 
@@ -299,6 +351,7 @@ def main() -> None:
                      "launches": gemm_launches, "avg_launch_us": 1000.0 * gemm_ms / max(gemm_launches, 1)},
         "turbo_4step_s": turbo_s,
         "graph_ms_per_step": graph_ms,
+        "encode_text": encode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))

@@ -4,6 +4,7 @@
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench gemm 4352 6400 2560
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench attention 1 20 5 4352
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench copy 1
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench encode-text 1 200
 
 ``fused-ops`` is the bandwidth microbenchmark of the row kernels at the single-stream block
 shape [1, 4352, 2560] BF16: RMSNorm + adaLN modulate, per-head qk-RMSNorm + 2-D RoPE for Q
@@ -145,6 +146,25 @@ def attention(b: int, h: int, hkv: int, n: int, iters: int = 20) -> dict:
             "mfma_frac": tflops / MFMA_TFLOPS}
 
 
+def encode_text(batch: int, real: int, iters: int = 10) -> dict:
+    """``HipIris.encode_text`` at full Iris-3B width (12 encoder layers of 2560, 300 tokens, the
+    first ``real`` of them unmasked) on seeded synthetic weights of a two-block model."""
+    from dataclasses import replace
+
+    from .config import IRIS_3B
+    from .engine import HipIris
+    from .weights import synthetic_state_dict
+
+    cfg = replace(IRIS_3B, depth=2, dual_depth=1, pixel=replace(IRIS_3B.pixel, depth=1))
+    engine = HipIris(cfg, synthetic_state_dict(cfg, device="cuda"), device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(0)
+    states = torch.randn(batch, cfg.text_len, cfg.text_lap_num_layers, cfg.text_dim, generator=g, device="cuda")
+    mask = torch.zeros(batch, cfg.text_len, dtype=torch.int64, device="cuda")
+    mask[:, :real] = 1
+    ms = _time(lambda i: engine.encode_text(states, mask), iters)
+    return {"op": "encode_text", "batch": batch, "tokens": cfg.text_len, "real": real, "ms": ms}
+
+
 def copy(gib: float, iters: int = 5) -> dict:
     src = torch.ones(int(gib * (1 << 28)), device="cuda", dtype=torch.float32)
     dst = torch.empty_like(src)
@@ -167,6 +187,9 @@ def main() -> None:
         p.add_argument(name, type=int)
     p = sub.add_parser("copy")
     p.add_argument("gib", type=float, nargs="?", default=1.0)
+    p = sub.add_parser("encode-text")
+    p.add_argument("batch", type=int, nargs="?", default=1)
+    p.add_argument("real", type=int, nargs="?", default=200)
     args = ap.parse_args()
     _lib.load()
     if args.cmd == "fused-ops":
@@ -175,6 +198,8 @@ def main() -> None:
         out = gemm(args.m, args.n, args.k, args.tile)
     elif args.cmd == "attention":
         out = attention(args.b, args.h, args.hkv, args.n)
+    elif args.cmd == "encode-text":
+        out = encode_text(args.batch, args.real)
     else:
         out = copy(args.gib)
     print(json.dumps(out))
