@@ -166,10 +166,12 @@ int iris_timestep_features(const float* t, const float* freqs, int batch, int ha
 
 /* Patchify + pixel embedding (src/iris_metal/model.py:188-189, 208-210; PixelEmbedder,
  * src/iris3b/nn/embeddings.py:291-328; pixel_rms_norm, src/iris_metal/kernels.py:217-232):
- * patches BF16 [batch, L, patch_stride] (first 3*p*p columns) in (channel, row, column) order;
- * pixels [batch*L, p*p, 16] = x W^T + b + sincos position (pos_x [W, 8], pos_y [H, 8]);
- * normed BF16 = rmsnorm(pixels) * norm_weight. */
-int iris_patchify_embed(const float* x, int batch, int height, int width, int patch, void* patches,
+ * x FP32 [batch, channels, H, W], channels 3, or 4 for the depth fine-tune's widened embedders
+ * (src/iris3b/downstream/depth.py:30-39); patches BF16 [batch, L, patch_stride] (first
+ * channels*p*p columns) in (channel, row, column) order; pixels [batch*L, p*p, 16] = x W^T + b +
+ * sincos position (W [16, channels], pos_x [W, 8], pos_y [H, 8]); normed BF16 =
+ * rmsnorm(pixels) * norm_weight. */
+int iris_patchify_embed(const float* x, int batch, int channels, int height, int width, int patch, void* patches,
                         long patch_stride, const float* pix_w, const float* pix_b, const float* pos_x, const float* pos_y,
                         const float* norm_weight, float eps, void* pixels, int pixels_dtype, void* normed,
                         hipStream_t stream);
@@ -187,9 +189,11 @@ int iris_pixel_mlp(void* pixels, int pixels_dtype, const void* branch, const voi
                    const float* next_norm_weight, void* next_input, long n_pixels, float eps, hipStream_t stream);
 
 /* Head + unpatchify (src/iris_metal/model.py:214-217): out[b, c, y, x] = h[pixel] . w[c] + bias[c]
- * for h BF16 [batch*L, p*p, 16] (pixels row-major in each patch), w FP32 [3, 16]. */
-int iris_unpatchify_head(const void* h, const float* w, const float* bias, float* out, int batch, int height,
-                         int width, int patch, hipStream_t stream);
+ * for h BF16 [batch*L, p*p, 16] (pixels row-major in each patch), w FP32 [out_channels, 16];
+ * out_channels 3, or 1 for the depth head (the 1x1 reducer of src/iris3b/downstream/depth.py:37,
+ * 47 folded into w and bias by the caller). */
+int iris_unpatchify_head(const void* h, const float* w, const float* bias, float* out, int out_channels, int batch,
+                         int height, int width, int patch, hipStream_t stream);
 
 /* s_cond = silu(t_emb + image) (src/iris_metal/model.py:207): out[r] = silu(x[r] + t[r / rows_per_batch]). */
 int iris_silu_add_rows(const float* x, const float* t, long rows, long rows_per_batch, int width, void* out,

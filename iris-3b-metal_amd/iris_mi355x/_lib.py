@@ -15,6 +15,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().with_name("libiris_hip.so")
 
+ABI_VERSION = 2  # iris_abi_version() of the library these signatures describe
 F32, BF16 = 0, 1
 EPI_NONE, EPI_SILU_MUL, EPI_SILU = 0, 1, 2
 ACT_NONE, ACT_SILU = 0, 1
@@ -43,10 +44,11 @@ _SIGNATURES: dict[str, list] = {
     "iris_gemm_bf16_grouped": [c_int, P, P, P, P, P, c_int, c_int, c_int, c_long, c_long, c_long, c_int, P],
     "iris_gemv_bf16": [P, P, c_int, c_int, c_int, P, P, c_int, P, c_int, c_int, P],
     "iris_timestep_features": [P, P, c_int, c_int, P, P],
-    "iris_patchify_embed": [P, c_int, c_int, c_int, c_int, P, c_long, P, P, P, P, P, c_float, P, c_int, P, P],
+    "iris_patchify_embed": [P, c_int, c_int, c_int, c_int, c_int, P, c_long, P, P, P, P, P, c_float, P, c_int, P,
+                            P],
     "iris_pixel_rms_norm": [P, c_int, P, P, c_long, c_float, P],
     "iris_pixel_mlp": [P, c_int, P, P, P, P, P, P, P, P, P, c_long, c_float, P],
-    "iris_unpatchify_head": [P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "iris_unpatchify_head": [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "iris_silu_add_rows": [P, P, c_long, c_long, c_int, P, c_int, P],
     "iris_copy_rows": [P, P, c_int, c_long, c_int, c_long, c_long, c_long, c_long, P],
     "iris_flow_euler": [P, P, c_long, c_float, c_float, P, P, P],
@@ -80,6 +82,9 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = c_int
+        if lib.iris_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIBRARY.name} has ABI {lib.iris_abi_version()}, these bindings need {ABI_VERSION}: "
+                               "rebuild it with __graft_entry__.build()")
         _lib = lib
     return _lib
 

@@ -10,7 +10,8 @@ namespace {
 constexpr int kPix = 16;      // pixel channel width of the PiT stage
 constexpr int kHidden = 64;   // PiT MLP hidden width
 
-template <typename TP>
+// C input channels: 3 (RGB) or 4 (the depth fine-tune's RGB + zero channel).
+template <typename TP, int C>
 __global__ __launch_bounds__(256) void patchify_embed_kernel(
     const float* __restrict__ x, int batch, int height, int width, int patch, bf16* __restrict__ patches,
     long patch_stride, const float* __restrict__ pix_w, const float* __restrict__ pix_b, const float* __restrict__ pos_x,
@@ -22,9 +23,9 @@ __global__ __launch_bounds__(256) void patchify_embed_kernel(
   const int px_x = static_cast<int>(idx % width);
   const int px_y = static_cast<int>((idx / width) % height);
   const long b = idx / hw;
-  float v[3];
+  float v[C];
 #pragma unroll
-  for (int c = 0; c < 3; ++c) v[c] = x[(b * 3 + c) * hw + static_cast<long>(px_y) * width + px_x];
+  for (int c = 0; c < C; ++c) v[c] = x[(b * C + c) * hw + static_cast<long>(px_y) * width + px_x];
   const int wp = width / patch;
   const long n_patches = static_cast<long>(height / patch) * wp;
   const long l = static_cast<long>(px_y / patch) * wp + px_x / patch;
@@ -32,13 +33,16 @@ __global__ __launch_bounds__(256) void patchify_embed_kernel(
   const int pp = patch * patch;
   bf16* prow = patches + (b * n_patches + l) * patch_stride + in_patch;
 #pragma unroll
-  for (int c = 0; c < 3; ++c) prow[c * pp] = from_f32<bf16>(v[c]);
+  for (int c = 0; c < C; ++c) prow[c * pp] = from_f32<bf16>(v[c]);
 
   float e[kPix];
   float ss = 0.0f;
 #pragma unroll
   for (int ch = 0; ch < kPix; ++ch) {
-    float acc = v[0] * pix_w[ch * 3 + 0] + v[1] * pix_w[ch * 3 + 1] + v[2] * pix_w[ch * 3 + 2] + pix_b[ch];
+    float acc = v[0] * pix_w[ch * C + 0];
+#pragma unroll
+    for (int c = 1; c < C; ++c) acc += v[c] * pix_w[ch * C + c];
+    acc += pix_b[ch];
     acc += ch < kPix / 2 ? pos_x[px_x * (kPix / 2) + ch] : pos_y[px_y * (kPix / 2) + ch - kPix / 2];
     e[ch] = acc;
     ss += acc * acc;
@@ -129,6 +133,8 @@ __global__ __launch_bounds__(256) void pixel_mlp_kernel(
   store8(next_input + idx * kPix + 8, h + 8);
 }
 
+// CO output channels: 3 (the predicted flow) or 1 (the depth head with its 1x1 reducer folded in).
+template <int CO>
 __global__ __launch_bounds__(256) void unpatchify_head_kernel(const bf16* __restrict__ h, const float* __restrict__ w,
                                                               const float* __restrict__ bias,
                                                               float* __restrict__ out, int batch, int height,
@@ -147,22 +153,36 @@ __global__ __launch_bounds__(256) void unpatchify_head_kernel(const bf16* __rest
   load8(h + q * kPix, v);
   load8(h + q * kPix + 8, v + 8);
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
+  for (int c = 0; c < CO; ++c) {
     float acc = 0.0f;
 #pragma unroll
     for (int ch = 0; ch < kPix; ++ch) acc += v[ch] * w[c * kPix + ch];
-    out[(b * 3 + c) * hw + static_cast<long>(px_y) * width + px_x] = acc + bias[c];
+    out[(b * CO + c) * hw + static_cast<long>(px_y) * width + px_x] = acc + bias[c];
   }
 }
 
 inline unsigned blocks_for(long n) { return static_cast<unsigned>((n + 255) / 256); }
+
+template <typename TP>
+void launch_patchify(int channels, unsigned blocks, hipStream_t stream, const float* x, int batch, int height,
+                     int width, int patch, bf16* patches, long patch_stride, const float* pix_w, const float* pix_b,
+                     const float* pos_x, const float* pos_y, const float* norm_w, float eps, TP* pixels,
+                     bf16* normed) {
+  if (channels == 4)
+    patchify_embed_kernel<TP, 4><<<blocks, 256, 0, stream>>>(x, batch, height, width, patch, patches, patch_stride,
+                                                             pix_w, pix_b, pos_x, pos_y, norm_w, eps, pixels, normed);
+  else
+    patchify_embed_kernel<TP, 3><<<blocks, 256, 0, stream>>>(x, batch, height, width, patch, patches, patch_stride,
+                                                             pix_w, pix_b, pos_x, pos_y, norm_w, eps, pixels, normed);
+}
 
 }  // namespace
 }  // namespace iris
 
 using namespace iris;
 
-extern "C" int iris_patchify_embed(const float* x, int batch, int height, int width, int patch, void* patches,
+extern "C" int iris_patchify_embed(const float* x, int batch, int channels, int height, int width, int patch,
+                                   void* patches,
                                    long patch_stride, const float* pix_w, const float* pix_b, const float* pos_x, const float* pos_y,
                                    const float* norm_weight, float eps, void* pixels, int pixels_dtype,
                                    void* normed, hipStream_t stream) {
@@ -171,19 +191,19 @@ extern "C" int iris_patchify_embed(const float* x, int batch, int height, int wi
                "patchify_embed: bad sizes");
   IRIS_REQUIRE(height % patch == 0 && width % patch == 0, "input %dx%d is not divisible by patch_size %d", height,
                width, patch);
-  IRIS_REQUIRE(patch_stride >= 3L * patch * patch, "patchify_embed: patch rows shorter than 3*p*p");
+  IRIS_REQUIRE(channels == 3 || channels == 4, "patchify_embed: 3 or 4 input channels (got %d)", channels);
+  IRIS_REQUIRE(patch_stride >= static_cast<long>(channels) * patch * patch,
+               "patchify_embed: patch rows shorter than channels*p*p");
   IRIS_REQUIRE(x && patches && pix_w && pix_b && pos_x && pos_y && norm_weight && pixels && normed,
                "patchify_embed: null pointer");
   const long n = static_cast<long>(batch) * height * width;
   if (n == 0) return IRIS_OK;
   if (pixels_dtype == IRIS_F32)
-    patchify_embed_kernel<float><<<blocks_for(n), 256, 0, stream>>>(x, batch, height, width, patch, (bf16*)patches, patch_stride,
-                                                                    pix_w, pix_b, pos_x, pos_y, norm_weight, eps,
-                                                                    (float*)pixels, (bf16*)normed);
+    launch_patchify<float>(channels, blocks_for(n), stream, x, batch, height, width, patch, (bf16*)patches,
+                           patch_stride, pix_w, pix_b, pos_x, pos_y, norm_weight, eps, (float*)pixels, (bf16*)normed);
   else
-    patchify_embed_kernel<bf16><<<blocks_for(n), 256, 0, stream>>>(x, batch, height, width, patch, (bf16*)patches, patch_stride,
-                                                                   pix_w, pix_b, pos_x, pos_y, norm_weight, eps,
-                                                                   (bf16*)pixels, (bf16*)normed);
+    launch_patchify<bf16>(channels, blocks_for(n), stream, x, batch, height, width, patch, (bf16*)patches,
+                          patch_stride, pix_w, pix_b, pos_x, pos_y, norm_weight, eps, (bf16*)pixels, (bf16*)normed);
   return check_launch("patchify_embed");
 }
 
@@ -223,14 +243,20 @@ extern "C" int iris_pixel_mlp(void* pixels, int pixels_dtype, const void* branch
   return check_launch("pixel_mlp");
 }
 
-extern "C" int iris_unpatchify_head(const void* h, const float* w, const float* bias, float* out, int batch,
-                                    int height, int width, int patch, hipStream_t stream) {
+extern "C" int iris_unpatchify_head(const void* h, const float* w, const float* bias, float* out, int out_channels,
+                                    int batch, int height, int width, int patch, hipStream_t stream) {
+  IRIS_REQUIRE(out_channels == 3 || out_channels == 1, "unpatchify_head: 3 or 1 output channels (got %d)",
+               out_channels);
   IRIS_REQUIRE(batch >= 0 && patch > 0 && height > 0 && width > 0 && height % patch == 0 && width % patch == 0,
                "unpatchify_head: bad sizes");
   IRIS_REQUIRE(h && w && bias && out, "unpatchify_head: null pointer");
   const long n = static_cast<long>(batch) * height * width;
   if (n == 0) return IRIS_OK;
-  unpatchify_head_kernel<<<blocks_for(n), 256, 0, stream>>>((const bf16*)h, w, bias, out, batch, height, width,
-                                                            patch);
+  if (out_channels == 1)
+    unpatchify_head_kernel<1><<<blocks_for(n), 256, 0, stream>>>((const bf16*)h, w, bias, out, batch, height, width,
+                                                                 patch);
+  else
+    unpatchify_head_kernel<3><<<blocks_for(n), 256, 0, stream>>>((const bf16*)h, w, bias, out, batch, height, width,
+                                                                 patch);
   return check_launch("unpatchify_head");
 }

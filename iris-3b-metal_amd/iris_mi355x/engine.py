@@ -138,8 +138,16 @@ class HipIris:
             w2p[:, : w2.shape[1]] = w2
             return bf(packed), bf(w2p)
 
-        # the patch embedder's K (3*p*p) is zero-padded to the GEMM's multiple of 64
+        # the patch embedder's K (C*p*p) is zero-padded to the GEMM's multiple of 64; C is 3, or 4
+        # for the depth fine-tune, whose embedders take an extra input channel after RGB
+        # (src/iris3b/downstream/depth.py:30-39)
         s_w = sd["s_embedder.proj.weight"].detach().float()
+        pp = cfg.patch_size ** 2
+        self.in_channels = s_w.shape[1] // pp
+        if s_w.shape[1] % pp or self.in_channels not in (3, 4):
+            raise ValueError(f"s_embedder.proj takes {s_w.shape[1]} features: not 3 or 4 channels of {pp} pixels")
+        if tuple(sd["pixel_embedder.proj.weight"].shape) != (K.PIXEL_WIDTH, self.in_channels):
+            raise ValueError("pixel_embedder.proj does not take the patch embedder's input channels")
         self.patch_k = _round_up(s_w.shape[1], 64)
         self.s_w = bf(torch.nn.functional.pad(s_w, (0, self.patch_k - s_w.shape[1])))
         self.s_b = f32("s_embedder.proj.bias")
@@ -194,6 +202,7 @@ class HipIris:
             })
         self.final_norm = f32("final_layer.norm.weight")
         self.final_w, self.final_b = f32("final_layer.linear.weight"), f32("final_layer.linear.bias")
+        self.out_channels = self.final_w.shape[0]
         self.t_freqs = tables.timestep_freqs(256, cfg.timestep_max_period, self.device)
         if "t_embedder.mlp.0.weight" in sd and sd["t_embedder.mlp.0.weight"].shape[1] != 256:
             raise ValueError("HipIris expects 256 timestep frequencies")
@@ -315,8 +324,8 @@ class HipIris:
         batch, channels, height, width = x.shape
         if height % p or width % p:
             raise ValueError(f"input {height}x{width} is not divisible by patch_size {p}")
-        if channels != cfg.in_channels:
-            raise ValueError(f"expected {cfg.in_channels} input channels, got {channels}")
+        if channels != self.in_channels:
+            raise ValueError(f"expected {self.in_channels} input channels, got {channels}")
         if text.dim() != 3 or text.shape[0] != batch or text.shape[2] != cfg.hidden_size:
             raise ValueError(f"text must be [B, T, {cfg.hidden_size}] prepared tokens, got {tuple(text.shape)}")
         if t.numel() != batch:
@@ -325,9 +334,10 @@ class HipIris:
         shape = _Shape(batch, height, width, text.shape[1])
         ws = self._workspace(shape)
         if out is None:
-            out = torch.empty(batch, 3, height, width, device=dev, dtype=torch.float32)
-        elif out.shape != x.shape or out.dtype != torch.float32 or not out.is_contiguous() or out.device != dev:
-            raise ValueError(f"out must be a contiguous FP32 {tuple(x.shape)} tensor on {dev}")
+            out = torch.empty(batch, self.out_channels, height, width, device=dev, dtype=torch.float32)
+        elif (out.shape != (batch, self.out_channels, height, width) or out.dtype != torch.float32
+              or not out.is_contiguous() or out.device != dev):
+            raise ValueError(f"out must be a contiguous FP32 {(batch, self.out_channels, height, width)} tensor on {dev}")
         if not self.graphs:
             x = x.to(dev, torch.float32).contiguous()
             t = t.reshape(batch).to(dev, torch.float32).contiguous()
@@ -335,10 +345,10 @@ class HipIris:
             self._forward(ws, x, t, text, out)
             return out
         if "graph" not in ws:
-            ws["x_in"] = torch.empty(batch, 3, height, width, device=dev, dtype=torch.float32)
+            ws["x_in"] = torch.empty(batch, self.in_channels, height, width, device=dev, dtype=torch.float32)
             ws["t_in"] = torch.empty(batch, device=dev, dtype=torch.float32)
             ws["text_in"] = torch.empty(text.shape, device=dev, dtype=torch.float32)
-            ws["out_ws"] = torch.empty(batch, 3, height, width, device=dev, dtype=torch.float32)
+            ws["out_ws"] = torch.empty(batch, self.out_channels, height, width, device=dev, dtype=torch.float32)
             ws["graph"] = None
         args = (ws, ws["x_in"], ws["t_in"], ws["text_in"], ws["out_ws"])
         ws["x_in"].copy_(x)
@@ -520,6 +530,20 @@ class HipIris:
         K.pixel_mlp_(ws["pixels"], ws["ex"].view_as(ws["hpix"]), ws["mods_pix"], blk["norm2"],
                      (blk["fc1_w"], blk["fc1_b"]), (blk["fc2_w"], blk["fc2_b"]), next_norm, eps,
                      next_input=ws["hpix"])
+
+    def fold_reducer(self, weight: torch.Tensor, bias: torch.Tensor) -> None:
+        """Fold a 1x1 convolution over the three output channels into the head (the depth
+        reducer, src/iris3b/downstream/depth.py:37, 47): the engine then returns
+        ``conv(v) = sum_c weight[0, c] v_c + bias`` as ``[B, 1, H, W]``, in one head pass."""
+        w = weight.detach().cpu().to(torch.float32).reshape(1, -1)
+        if w.shape[1] != self.out_channels or self.out_channels != 3 or bias.numel() != 1:
+            raise ValueError("fold_reducer takes a [1, 3, 1, 1] convolution and its bias over the 3-channel head")
+        b = bias.detach().cpu().to(torch.float32).reshape(1)
+        head_w, head_b = self.final_w.cpu(), self.final_b.cpu()
+        self.final_w = (w @ head_w).to(self.device).contiguous()
+        self.final_b = (w @ head_b + b).to(self.device).contiguous()
+        self.out_channels = 1
+        self._ws = None  # the output buffers and any recorded graph change shape
 
     def as_dit(self) -> "HipIrisDiT":
         """The upstream ``IrisDiT`` call surface over this engine (the Turbo route)."""

@@ -525,16 +525,19 @@ def patchify_embed(x, patch, pix_w, pix_b, pos_x, pos_y, norm_weight, eps, patch
     (src/iris_metal/model.py:188-189, 208-210)."""
     batch, channels, height, width = x.shape
     _on_gpu(x, patches, pixels, normed)
-    _require(channels == 3 and x.dtype == torch.float32 and x.is_contiguous(), "patchify_embed: FP32 [B, 3, H, W]")
+    _require(channels in (3, 4) and x.dtype == torch.float32 and x.is_contiguous(),
+             "patchify_embed: FP32 [B, 3 or 4, H, W]")
     _require_fp32(pix_w=pix_w, pix_b=pix_b, pos_x=pos_x, pos_y=pos_y, norm_weight=norm_weight)
+    _require(pix_w.shape == (PIXEL_WIDTH, channels), f"patchify_embed: pixel embedder weight must be [16, {channels}]")
     n_patches = (height // patch) * (width // patch)
     _require(patches.dtype == torch.bfloat16 and patches.stride(-1) == 1
              and patches.reshape(-1, patches.shape[-1]).shape[0] == batch * n_patches
-             and patches.shape[-1] >= 3 * patch * patch, "patchify_embed: patches must be BF16 [B*L, >= 3*p*p]")
+             and patches.shape[-1] >= channels * patch * patch,
+             "patchify_embed: patches must be BF16 [B*L, >= C*p*p]")
     _require(pixels.numel() == normed.numel() == batch * height * width * PIXEL_WIDTH
              and normed.dtype == torch.bfloat16, "patchify_embed: bad pixel buffers")
     L.call(
-        "iris_patchify_embed", L.ptr(x), batch, height, width, patch, L.ptr(patches), patches.stride(-2),
+        "iris_patchify_embed", L.ptr(x), batch, channels, height, width, patch, L.ptr(patches), patches.stride(-2),
         L.ptr(pix_w), L.ptr(pix_b),
         L.ptr(pos_x), L.ptr(pos_y), L.ptr(norm_weight), float(eps), L.ptr(pixels), L.dtype_code(pixels.dtype),
         L.ptr(normed), L.stream(),
@@ -542,14 +545,17 @@ def patchify_embed(x, patch, pix_w, pix_b, pos_x, pos_y, norm_weight, eps, patch
 
 
 def unpatchify_head(h, weight, bias, out, patch) -> torch.Tensor:
-    """``out[b, c, y, x] = h[pixel] . weight[c] + bias[c]`` (src/iris_metal/model.py:214-217)."""
+    """``out[b, c, y, x] = h[pixel] . weight[c] + bias[c]`` (src/iris_metal/model.py:214-217);
+    3 output channels, or 1 for the depth head."""
     batch, channels, height, width = out.shape
     _on_gpu(h, weight, bias, out)
-    _require(channels == 3 and out.dtype == torch.float32 and out.is_contiguous(), "unpatchify_head: FP32 output")
+    _require(channels in (1, 3) and out.dtype == torch.float32 and out.is_contiguous(),
+             "unpatchify_head: FP32 output of 1 or 3 channels")
     _require(h.dtype == torch.bfloat16 and h.is_contiguous(), "unpatchify_head: BF16 pixels")
     _require_fp32(weight=weight, bias=bias)
-    L.call("iris_unpatchify_head", L.ptr(h), L.ptr(weight), L.ptr(bias), L.ptr(out), batch, height, width, patch,
-           L.stream())
+    _require(weight.shape == (channels, PIXEL_WIDTH) and bias.numel() == channels, "unpatchify_head: head shape")
+    L.call("iris_unpatchify_head", L.ptr(h), L.ptr(weight), L.ptr(bias), L.ptr(out), channels, batch, height, width,
+           patch, L.stream())
     return out
 
 

@@ -215,17 +215,19 @@ def parameter_count(cfg: ModelConfig) -> int:
 
 
 def synthetic_state_dict(
-    cfg: ModelConfig, seed: int = 0, std: float = 0.02, device: str | torch.device = "cpu"
+    cfg: ModelConfig, seed: int = 0, std: float = 0.02, device: str | torch.device = "cpu",
+    schema: dict[str, ParamSpec] | None = None,
 ) -> dict[str, torch.Tensor]:
     """FP32 weights by the seeded recipe above, in sorted key order.
 
     ``device`` selects where the generator draws; ``"cpu"`` is the canonical
     recipe, and a device generator gives a different (but again deterministic)
-    draw that is much faster for the 3B-parameter model.
+    draw that is much faster for the 3B-parameter model. ``schema`` replaces the
+    denoiser's parameter schema (the downstream task models).
     """
     gen = torch.Generator(device=device).manual_seed(seed)
     out: dict[str, torch.Tensor] = {}
-    for name, spec in sorted(parameter_schema(cfg).items()):
+    for name, spec in sorted((parameter_schema(cfg) if schema is None else schema).items()):
         t = torch.randn(spec.shape, generator=gen, device=device, dtype=torch.float32)
         if spec.kind == "pos":
             pass

@@ -19,6 +19,10 @@ identity, zero-gate halving, sandwich-norm RMS, keep/drop equality,
 parameter count) and by library routines (unfold/fold); the reference's own
 ``IrisDiT`` cannot be imported here (its config module needs omegaconf, which
 is absent), so their composed output is otherwise "parity unpinned".
+The downstream wrappers ``depth_forward`` and ``restore_tile`` are pinned by
+invariants of their own (``tests/test_tasks.py``): the zero fourth channel
+equals the three-channel model with the sliced embedders, and a head that
+predicts a constant flow moves every pixel by exactly ``-sigma`` times it.
 """
 
 from __future__ import annotations
@@ -454,6 +458,32 @@ def forward(p: Params, cfg, x: Tensor, t: Tensor, y: Tensor | None = None, y_mas
 # samplers (src/iris3b/sampling.py:98-138, src/iris3b/flow/solver.py, schedule.py:24-25)
 # ----------------------------------------------------------------------------
 TURBO_SIGMAS = (1.0, 0.938, 0.833, 0.625)
+
+
+# ----------------------------------------------------------------------------
+# downstream tasks (src/iris3b/downstream/depth.py, restoration.py)
+# ----------------------------------------------------------------------------
+def depth_forward(p: Params, cfg, rgb: Tensor, embeddings: Tensor, mask: Tensor,
+                  num_train_timesteps: int = 1000) -> Tensor:
+    """``IrisDepth.forward`` (depth.py:41-48): RGB plus a zero channel after it into the widened
+    embedders of the ``pixel.*`` denoiser at model time ``num_train_timesteps`` with the (empty)
+    prompt, then the 1x1 ``depth_reducer`` -> ``[B, 1, H, W]``."""
+    b, _, h, w = rgb.shape
+    sub = {k[len("pixel."):]: v for k, v in p.items() if k.startswith("pixel.")}
+    x = torch.cat([rgb.float(), torch.zeros(b, 1, h, w)], dim=1)
+    t = torch.full((b,), float(num_train_timesteps))
+    out = forward(sub, cfg, x, t, embeddings.expand(b, *embeddings.shape[1:]), y_mask=mask.expand(b, -1))
+    return F.conv2d(out, p["depth_reducer.weight"], p["depth_reducer.bias"])
+
+
+def restore_tile(p: Params, cfg, x: Tensor, embeddings: Tensor, mask: Tensor, sigma: float,
+                 num_train_timesteps: int = 1000) -> Tensor:
+    """``Restorer.restore_tile`` (restoration.py:135-142): one forward at model time
+    ``sigma * num_train_timesteps`` with the (empty) prompt, then ``x - sigma * v``."""
+    t = torch.full((x.shape[0],), sigma * num_train_timesteps)
+    y = embeddings.expand(len(x), *embeddings.shape[1:])
+    v = forward(p, cfg, x, t, y, y_mask=mask.expand(len(x), -1))
+    return x.float() - sigma * v.float()
 
 
 def turbo_sample(model_fn, noise: Tensor, sigmas=TURBO_SIGMAS, num_train_timesteps: int = 1000,

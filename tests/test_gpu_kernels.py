@@ -402,19 +402,23 @@ def test_timestep_features():
     torch.testing.assert_close(out.cpu(), O.timestep_features(t, 256, 10.0), rtol=0, atol=2e-6)
 
 
-@pytest.mark.parametrize("hw,patch", [((32, 48), 4), ((64, 64), 16)])
-def test_patchify_embed_and_head(hw, patch):
+@pytest.mark.parametrize("hw,patch,channels,out_channels", [((32, 48), 4, 3, 3), ((64, 64), 16, 3, 3),
+                                                             ((32, 48), 16, 4, 1), ((64, 32), 4, 4, 3)])
+def test_patchify_embed_and_head(hw, patch, channels, out_channels):
+    """3-channel RGB and the depth fine-tune's 4-channel input; the 3-channel flow head and the
+    1-channel depth head."""
     from iris_mi355x import tables
 
     b = 2
     h, w = hw
     g = gen(12)
-    x = torch.randn(b, 3, h, w, generator=g)
-    p = {"pixel_embedder.proj.weight": 0.5 * torch.randn(16, 3, generator=g),
+    x = torch.randn(b, channels, h, w, generator=g)
+    p = {"pixel_embedder.proj.weight": 0.5 * torch.randn(16, channels, generator=g),
          "pixel_embedder.proj.bias": 0.1 * torch.randn(16, generator=g)}
     nw = 1 + 0.02 * torch.randn(16, generator=g)
     n_patches = (h // patch) * (w // patch)
-    kp = (3 * patch * patch + 63) // 64 * 64
+    k = channels * patch * patch
+    kp = (k + 63) // 64 * 64
     patches = torch.zeros(b * n_patches, kp, device=DEV, dtype=torch.bfloat16)
     pixels = torch.empty(b * n_patches, patch * patch, 16, device=DEV)
     normed = torch.empty_like(pixels, dtype=torch.bfloat16)
@@ -422,15 +426,15 @@ def test_patchify_embed_and_head(hw, patch):
     K.patchify_embed(x.to(DEV), patch, p["pixel_embedder.proj.weight"].to(DEV), p["pixel_embedder.proj.bias"].to(DEV),
                      pos_x, pos_y, nw.to(DEV), 1e-6, patches, pixels, normed)
     want_patches = O.patchify(x, patch).reshape(b * n_patches, -1)
-    assert torch.equal(patches[:, :3 * patch * patch].cpu(), want_patches.to(torch.bfloat16))
-    assert torch.all(patches[:, 3 * patch * patch:] == 0)
+    assert torch.equal(patches[:, :k].cpu(), want_patches.to(torch.bfloat16))
+    assert torch.all(patches[:, k:] == 0)
     want_pix = O.pixel_embed(p, x, patch, True)
     torch.testing.assert_close(pixels.cpu(), want_pix, rtol=1e-5, atol=1e-5)
     close_bf16(normed, O.rms_norm(want_pix, nw, 1e-6))
 
-    hw_ = 0.3 * torch.randn(3, 16, generator=g)
-    hb = 0.1 * torch.randn(3, generator=g)
-    out = torch.empty(b, 3, h, w, device=DEV)
+    hw_ = 0.3 * torch.randn(out_channels, 16, generator=g)
+    hb = 0.1 * torch.randn(out_channels, generator=g)
+    out = torch.empty(b, out_channels, h, w, device=DEV)
     K.unpatchify_head(normed, hw_.to(DEV), hb.to(DEV), out, patch)
     want = O.unpatchify(normed.float().cpu() @ hw_.T + hb, b, h, w, patch)
     torch.testing.assert_close(out.cpu(), want, rtol=1e-5, atol=1e-5)

@@ -45,7 +45,9 @@ def test_binding_covers_the_header():
 
 
 def test_abi_version(lib):
-    assert lib.iris_abi_version() == 1
+    from iris_mi355x import _lib
+
+    assert lib.iris_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_build_recipe_targets_gfx950_without_packed_fp32():
@@ -70,5 +72,10 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
         _lib.call("iris_flash_attn", 1 << 20, 1 << 20, 1 << 20, 1, 6, 2, 64, 64, 0, 0.1, None, 1 << 20, 768, 0,
                   64, None, None, 0, 0, 0, None)
     with pytest.raises(ValueError, match="not divisible"):
-        _lib.call("iris_patchify_embed", 1 << 20, 1, 30, 32, 16, 1 << 20, 768, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
+        _lib.call("iris_patchify_embed", 1 << 20, 1, 3, 30, 32, 16, 1 << 20, 768, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
                   1 << 20, 1e-6, 1 << 20, _lib.F32, 1 << 20, None)
+    with pytest.raises(ValueError, match="3 or 4 input channels"):
+        _lib.call("iris_patchify_embed", 1 << 20, 1, 5, 32, 32, 16, 1 << 20, 1280, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
+                  1 << 20, 1e-6, 1 << 20, _lib.F32, 1 << 20, None)
+    with pytest.raises(ValueError, match="3 or 1 output channels"):
+        _lib.call("iris_unpatchify_head", 1 << 20, 1 << 20, 1 << 20, 1 << 20, 2, 1, 32, 32, 16, None)
