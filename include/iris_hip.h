@@ -95,7 +95,8 @@ int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int
 /* Tuning hook for the benchmark sweep: force the attention variant (32 query rows per wave in
  * all; 0: 64-key tiles staged through registers, 1: 32-key tiles staged through registers,
  * 2: 64-key tiles in a 2-stage global_load_lds ring, 3: 32-key tiles in a 3-stage ring) or
- * restore the automatic choice (-1).
+ * restore the automatic choice (-1: variant 1 when four or more query heads share a K/V head,
+ * else variant 2).
  * No counterpart in the reference. */
 int iris_flash_attn_force_variant(int variant);
 

@@ -283,34 +283,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
         }
     }
 
-    // online softmax in the log2 domain, one query column per lane (and its partner lane ^ 32)
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[qb], mx * sl2);
-      // (a column with no key so far keeps m = -inf; exponents are then taken against 0)
-      const float m_use = MASKED && m_new == -INFINITY ? 0.0f : m_new;
-      if (__any(m_new != m_run[qb])) {  // wave-uniform branch; alpha is 1 where the max held
-        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
-        l_run[qb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
-        m_run[qb] = m_new;
-      }
+    // Online softmax in the log2 domain, one query column per lane (and its partner lane ^ 32),
+    // against the running max m_run, which is raised lazily: while every probability of the
+    // tile stays <= 2^8 (each lane's partial sum <= 256) m_run and the output stay as they are;
+    // otherwise (the first tile, a score more than 8 above m_run, a column with no key yet) the
+    // columns that need it take their exact maxima, rescale their output and sums, and
+    // recompute (the other columns keep their reference, so a column's result never depends on
+    // its neighbours, padding rows included). The common path has no max reduction and no
+    // output rescale. The sums add the BF16
+    // probabilities the P.V product uses (v_dot2 with ones, two per instruction), so the
+    // normalisation matches the numerator.
+    bf16x8 pf[KB][2][QB];
+    const bf16x2 ones = {static_cast<bf16>(1.0f), static_cast<bf16>(1.0f)};
+    auto probs = [&](int qb, float m) {
       float sum = 0.0f;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = __builtin_amdgcn_exp2f(s[kb][qb][r] * sl2 - m_use);
-          s[kb][qb][r] = pv;
-          sum += pv;
+        for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            pf[kb][jj][qb][e] = from_f32<bf16>(__builtin_amdgcn_exp2f(s[kb][qb][8 * jj + e] * sl2 - m));
+#pragma unroll
+          for (int e = 0; e < 8; e += 2)
+            sum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pf[kb][jj][qb][e], pf[kb][jj][qb][e + 1]}, ones, sum, false);
         }
+      return sum;
+    };
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      float sum = probs(qb, m_run[qb]);
+      const int need = !(sum <= 256.0f);  // also for NaN / inf partial sums (the first tile)
+      if (__any(need)) {                  // wave-uniform branch
+        const int partner = __shfl_xor(need, 32);  // (every lane takes part in the exchange)
+        const bool raise = need || partner;         // both halves of the column
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_max = fmaxf(m_run[qb], mx * sl2);
+        // (a column with no key so far takes a finite reference, so masked tiles give 0, not NaN)
+        const float m_new = !raise ? m_run[qb] : (MASKED && m_max == -INFINITY ? 0.0f : m_max);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);  // exactly 1 unless raised
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
+        m_run[qb] = m_new;
+        sum = probs(qb, m_new);
+      }
       l_run[qb] += sum;
     }
 
@@ -320,11 +342,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
     for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
-        bf16x8 pf[QB];
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) pf[qb][e] = from_f32<bf16>(s[kb][qb][8 * jj + e]);
         const int c = 4 * kb + 2 * jj + g;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
@@ -332,7 +349,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
           const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vl + d * KVT + 8 * (c ^ swz<VCPR>(d)));
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-            o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qb], o[db][qb], 0, 0, 0);
+            o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][jj][qb], o[db][qb], 0, 0, 0);
         }
       }
     }
@@ -409,9 +426,11 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   args.n_pad = static_cast<int>(n_pad);
   args.n_split = static_cast<int>(n_split);
   args.hpw = group < 4 ? group : 4;
-  // 32-row waves at two workgroups per CU measured fastest at every Iris shape (trunk 4352 and
-  // 1280 tokens, pixel 4096): the softmax of one workgroup overlaps the MFMAs of the other.
-  const int variant = g_attn_variant >= 0 ? g_attn_variant : 0;
+  // Grouped heads (the trunk's 20 query / 5 K/V heads): 32-key tiles staged through registers
+  // (168 VGPRs, three workgroups per CU, so the 680 workgroups of a 4352-token batch run in
+  // one round); one query head per K/V head (the pixel stage): 64-key tiles in a global_load_lds
+  // ring. Both measured fastest at their shapes.
+  const int variant = g_attn_variant >= 0 ? g_attn_variant : (group >= 4 ? 1 : 2);
   const Variant v = kVariants[variant];
   args.rows_per_wg = 32 * v.qb * 4 / args.hpw;
   args.n_qblocks = static_cast<int>((n + args.rows_per_wg - 1) / args.rows_per_wg);

@@ -242,6 +242,26 @@ def test_flash_attention_small(b, h, hkv, n):
     close_bf16(out.view(b, n, -1), want, scale=1.0, floor=4e-3)
 
 
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+def test_flash_attention_rows_do_not_depend_on_padding_rows(variant):
+    """A query row's output is bit-identical whatever the padding query rows (>= n) hold: the
+    lazy max raise is decided per column, not per wave."""
+    b, h, hkv, n = 1, 8, 2, 77
+    q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 17)
+    outs = []
+    _lib.call("iris_flash_attn_force_variant", variant)
+    try:
+        for fill in (0.0, 300.0, float("nan")):
+            qf = qd.clone()
+            qf[:, :, n:] = fill
+            out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+            K.flash_attention(qf, kd, vt, n, None, out, n_split=0)
+            outs.append(out.cpu())
+    finally:
+        _lib.call("iris_flash_attn_force_variant", -1)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 def test_flash_attention_trunk_shape_with_gate_and_split():
     """20 query / 5 K/V heads over 256 text + 4096 image tokens, gate fused, rows split."""
     b, h, hkv, t, l = 1, 20, 5, 256, 4096
