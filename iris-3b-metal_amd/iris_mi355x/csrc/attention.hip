@@ -376,8 +376,9 @@ struct Variant {
 };
 // 0: 32 query rows per wave, 64-key tiles staged through registers; 1: the same with 32-key
 // tiles; 2: 64-key tiles, 2-stage global_load_lds ring; 3: 32-key tiles, 3-stage ring.
-// (An eight-wave ping-pong of MFMA and softmax phases measured 1.8x slower at the trunk shape
-// and was dropped.)
+// (Measured and dropped: an eight-wave ping-pong of MFMA and softmax phases, 1.8x slower at the
+// trunk shape; a software-pipelined wave issuing tile t - 1's P.V MFMAs around tile t's softmax,
+// no faster than variant 1; 64- and 96-row waves at one wave per SIMD, 1.5-1.9x slower.)
 constexpr Variant kVariants[] = {{1, 2, 64, true}, {1, 2, 32, true}, {1, 2, 64, false}, {1, 3, 32, false}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 int g_attn_variant = -1;
