@@ -11,13 +11,31 @@
 namespace iris {
 namespace {
 
-constexpr int kRowsPerWave = 1;                   // rows a wave walks through
-constexpr int kRowsPerBlock = 4 * kRowsPerWave;    // 4 waves per 256-thread workgroup
+constexpr int kRowsPerBlock = 4;  // one row per wave, 4 waves per 256-thread workgroup
 
-// NC = 8-element chunks each lane holds (width <= NC * 512). Every wave walks kRowsPerWave
-// consecutive rows and keeps the per-column coefficients (gain * (1 + scale), shift) in
-// registers while they stay in one batch: the FP32 vectors are read once per wave, not once
-// per row, so the kernel's L2 traffic stays close to its HBM traffic.
+// 8 elements of a row held in their storage type (BF16 rows take half the registers of FP32
+// ones, which keeps more waves, and more loads in flight, per CU).
+template <typename T>
+struct Chunk8;
+template <>
+struct Chunk8<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ float operator[](int e) const { return to_f32(v[e]); }
+};
+template <>
+struct Chunk8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ float operator[](int e) const { return e < 4 ? a[e] : b[e - 4]; }
+};
+
+// NC = 8-element chunks each lane holds (width <= NC * 512). A wave issues its row's loads
+// first, reduces, and reads the per-column FP32 coefficients (gain, scale, shift; L2 hits) chunk
+// by chunk in the output pass, so they need no registers across the row.
 template <int NC, typename TI, typename TO>
 __global__ __launch_bounds__(256) void rms_norm_modulate_kernel(const TI* __restrict__ x, TO* __restrict__ out,
                                                                 const float* __restrict__ weight,
@@ -25,53 +43,38 @@ __global__ __launch_bounds__(256) void rms_norm_modulate_kernel(const TI* __rest
                                                                 const float* __restrict__ scale, long rows,
                                                                 long rows_per_batch, int width, long mod_stride,
                                                                 float eps) {
-  const long row0 = (static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int nc = width >> 3;
-  float c1[NC][8], c0[NC][8];
-  long cur_b = -1;
-  for (int k = 0; k < kRowsPerWave; ++k) {
-    const long row = row0 + k;
-    if (row >= rows) return;
-    const long b = row / rows_per_batch;
-    if (b != cur_b) {  // wave-uniform
-      cur_b = b;
+  Chunk8<TI> v[NC];
 #pragma unroll
-      for (int i = 0; i < NC; ++i) {
-        const int j = lane + i * kWave;
-        if (j < nc) {
-          float w[8], s1[8];
-          load8(weight + 8 * j, w);
-          load8(scale + b * mod_stride + 8 * j, s1);
-          load8(shift + b * mod_stride + 8 * j, c0[i]);
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc) v[i].load(x + row * width + 8 * j);
+  }
+  float ss = 0.0f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) c1[i][e] = w[e] * (1.0f + s1[e]);
-        }
-      }
-    }
-    const TI* xr = x + row * width;
-    float v[NC][8];
-    float ss = 0.0f;
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc)
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      const int j = lane + i * kWave;
-      if (j < nc) {
-        load8(xr + 8 * j, v[i]);
+      for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+  }
+  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
+  const long b = row / rows_per_batch;
+  TO* o = out + row * width;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
-      }
-    }
-    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
-    TO* o = out + row * width;
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc) {
+      float w[8], s1[8], c0[8], y[8];
+      load8(weight + 8 * j, w);
+      load8(scale + b * mod_stride + 8 * j, s1);
+      load8(shift + b * mod_stride + 8 * j, c0);
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      const int j = lane + i * kWave;
-      if (j < nc) {
-        float y[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = (v[i][e] * r) * c1[i][e] + c0[i][e];
-        store8(o + 8 * j, y);
-      }
+      for (int e = 0; e < 8; ++e) y[e] = (v[i][e] * r) * (w[e] * (1.0f + s1[e])) + c0[e];
+      store8(o + 8 * j, y);
     }
   }
 }
@@ -87,78 +90,61 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(
     const float* __restrict__ gate, long rows, long rows_per_batch, int width, long mod_stride, float eps,
     const float* __restrict__ next_weight, const float* __restrict__ next_shift,
     const float* __restrict__ next_scale, long next_mod_stride, TO* __restrict__ next_out) {
-  const long row0 = (static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
+  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int nc = width >> 3;
-  const bool fused = next_out != nullptr;
-  float gw[NC][8], c1[NC][8], c0[NC][8];
-  long cur_b = -1;
-  for (int k = 0; k < kRowsPerWave; ++k) {
-    const long row = row0 + k;
-    if (row >= rows) return;
-    const long b = row / rows_per_batch;
-    if (b != cur_b) {  // wave-uniform
-      cur_b = b;
+  Chunk8<TB> v[NC];
+  float x[NC][8];
+  float* res = residual + row * width;
 #pragma unroll
-      for (int i = 0; i < NC; ++i) {
-        const int j = lane + i * kWave;
-        if (j < nc) {
-          float w[8], g[8];
-          load8(weight + 8 * j, w);
-          load8(gate + b * mod_stride + 8 * j, g);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) gw[i][e] = g[e] * w[e];
-          if (fused) {
-            float w2[8], s1[8];
-            load8(next_weight + 8 * j, w2);
-            load8(next_scale + b * next_mod_stride + 8 * j, s1);
-            load8(next_shift + b * next_mod_stride + 8 * j, c0[i]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) c1[i][e] = w2[e] * (1.0f + s1[e]);
-          }
-        }
-      }
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc) {
+      v[i].load(branch + row * width + 8 * j);
+      load8(res + 8 * j, x[i]);
     }
-    const TB* br = branch + row * width;
-    float* res = residual + row * width;
-    float v[NC][8], x[NC][8];
-    float ss = 0.0f;
+  }
+  float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      const int j = lane + i * kWave;
-      if (j < nc) {
-        load8(br + 8 * j, v[i]);
-        load8(res + 8 * j, x[i]);
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+      for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+  }
+  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
+  const long b = row / rows_per_batch;
+  float ss2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc) {
+      float w[8], g[8];
+      load8(weight + 8 * j, w);
+      load8(gate + b * mod_stride + 8 * j, g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[i][e] += (g[e] * w[e]) * (v[i][e] * r);
+        ss2 += x[i][e] * x[i][e];
       }
+      store8(res + 8 * j, x[i]);
     }
-    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(width) + eps);
-    float ss2 = 0.0f;
+  }
+  if (next_out == nullptr) return;
+  const float r2 = rsqrtf(wave_sum(ss2) / static_cast<float>(width) + eps);
+  TO* o = next_out + row * width;
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      const int j = lane + i * kWave;
-      if (j < nc) {
+  for (int i = 0; i < NC; ++i) {
+    const int j = lane + i * kWave;
+    if (j < nc) {
+      float w2[8], s1[8], c0[8], y[8];
+      load8(next_weight + 8 * j, w2);
+      load8(next_scale + b * next_mod_stride + 8 * j, s1);
+      load8(next_shift + b * next_mod_stride + 8 * j, c0);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          x[i][e] += gw[i][e] * (v[i][e] * r);
-          ss2 += x[i][e] * x[i][e];
-        }
-        store8(res + 8 * j, x[i]);
-      }
-    }
-    if (!fused) continue;
-    const float r2 = rsqrtf(wave_sum(ss2) / static_cast<float>(width) + eps);
-    TO* o = next_out + row * width;
-#pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      const int j = lane + i * kWave;
-      if (j < nc) {
-        float y[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = (x[i][e] * r2) * c1[i][e] + c0[i][e];
-        store8(o + 8 * j, y);
-      }
+      for (int e = 0; e < 8; ++e) y[e] = (x[i][e] * r2) * (w2[e] * (1.0f + s1[e])) + c0[e];
+      store8(o + 8 * j, y);
     }
   }
 }
