@@ -76,6 +76,17 @@ int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int dst_dtype, 
 int iris_v_heads_t(const void* src, void* dst, int batch, long n_src, long n_dst, int heads, long dst_offset,
                    long row_stride, long col_offset, hipStream_t stream);
 
+/* The three attention-input calls of one BF16 projection in one launch (the reference makes
+ * them separately: qk_norm_rope on Q and on K, src/iris_metal/model.py:236-250, and the V
+ * layout): iris_qk_norm_rope of the `heads` Q heads at q_col into q and of the `kv_heads` K
+ * heads at k_col into k (gains q_weight / k_weight, rows at dst_offset + t of n_dst), and
+ * iris_v_heads_t of the `kv_heads` V heads at v_col into vt (n_vt positions). Same results as
+ * the three calls, all BF16. */
+int iris_qkv_prepare(const void* src, void* q, void* k, void* vt, const float* q_weight, const float* k_weight,
+                     const float* cos_table, const float* sin_table, long table_rows, int batch, long n_src,
+                     long n_dst, long n_vt, int heads, int kv_heads, long dst_offset, long row_stride, long q_col,
+                     long k_col, long v_col, float eps, hipStream_t stream);
+
 /* softmax(q k^T * scale) v over a joint sequence of n tokens (F.scaled_dot_product_attention
  * with GQA, src/iris_metal/model.py:243-250; src/iris3b/nn/attention.py:61-91).
  * q: BF16 [batch, heads, n_pad, 128]; k: BF16 [batch, kv_heads, n_pad, 128];

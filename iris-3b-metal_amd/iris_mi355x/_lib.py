@@ -15,7 +15,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().with_name("libiris_hip.so")
 
-ABI_VERSION = 2  # iris_abi_version() of the library these signatures describe
+ABI_VERSION = 3  # iris_abi_version() of the library these signatures describe
 F32, BF16 = 0, 1
 EPI_NONE, EPI_SILU_MUL, EPI_SILU = 0, 1, 2
 ACT_NONE, ACT_SILU = 0, 1
@@ -31,6 +31,8 @@ _SIGNATURES: dict[str, list] = {
     "iris_qk_norm_rope": [P, c_int, P, c_int, P, P, P, c_long, c_int, c_long, c_long, c_int, c_long, c_long,
                           c_long, c_float, P],
     "iris_v_heads_t": [P, P, c_int, c_long, c_long, c_int, c_long, c_long, c_long, P],
+    "iris_qkv_prepare": [P, P, P, P, P, P, P, P, c_long, c_int, c_long, c_long, c_long, c_int, c_int, c_long,
+                         c_long, c_long, c_long, c_long, c_float, P],
     "iris_flash_attn": [P, P, P, c_int, c_int, c_int, c_long, c_long, c_long, c_float, P, P, c_long, c_long,
                         c_long, P, P, c_long, c_long, c_long, P],
     "iris_gemm_bf16": [P, P, P, P, c_int, c_int, c_int, c_int, c_long, c_long, c_long, c_int, P],

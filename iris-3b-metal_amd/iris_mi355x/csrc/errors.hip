@@ -28,4 +28,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* iris_last_error(void) { return g_message; }
 
-extern "C" int iris_abi_version(void) { return 2; }
+extern "C" int iris_abi_version(void) { return 3; }

@@ -154,18 +154,18 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(
 // before the first reduction, the token's rotary row read once), 16 groups per workgroup.
 constexpr int kQkRows = 4;
 
+// Workgroup `block` of batch `b` (16 groups of 16 lanes).
 template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict__ src, TO* __restrict__ dst,
-                                                           const float* __restrict__ weight,
-                                                           const float* __restrict__ cos_table,
-                                                           const float* __restrict__ sin_table, long n_src,
-                                                           long n_dst, int heads, long dst_offset, long row_stride,
-                                                           long col_offset, float eps) {
+__device__ __forceinline__ void qk_norm_rope_block(const TI* __restrict__ src, TO* __restrict__ dst,
+                                                   const float* __restrict__ weight,
+                                                   const float* __restrict__ cos_table,
+                                                   const float* __restrict__ sin_table, long n_src, long n_dst,
+                                                   int heads, long dst_offset, long row_stride, long col_offset,
+                                                   float eps, long block, long b) {
   // group = (token, up to kQkRows consecutive heads): the rotary row is read once per group
   const int head_groups = (heads + kQkRows - 1) / kQkRows;
-  const long grp = static_cast<long>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const long grp = block * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
-  const long b = blockIdx.y;
   if (grp >= n_src * head_groups) return;  // whole 16-lane groups leave together
   const long token = grp / head_groups;
   const int head0 = static_cast<int>(grp - token * head_groups) * kQkRows;
@@ -198,6 +198,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict_
   }
 }
 
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict__ src, TO* __restrict__ dst,
+                                                           const float* __restrict__ weight,
+                                                           const float* __restrict__ cos_table,
+                                                           const float* __restrict__ sin_table, long n_src,
+                                                           long n_dst, int heads, long dst_offset, long row_stride,
+                                                           long col_offset, float eps) {
+  qk_norm_rope_block<TI, TO>(src, dst, weight, cos_table, sin_table, n_src, n_dst, heads, dst_offset, row_stride,
+                             col_offset, eps, blockIdx.x, blockIdx.y);
+}
+
 // Position of token slot i inside its group of 16 in the V^T layout the attention kernel reads:
 // the middle two 4-token quads are swapped (0-3, 8-11, 4-7, 12-15), so that the 8 keys one
 // MFMA lane needs (4 g .. 4 g + 3 and 8 + 4 g .. 8 + 4 g + 3) are contiguous. An involution.
@@ -209,14 +220,13 @@ __device__ __forceinline__ int vt_slot(int i) {
 // Transpose the V heads into dst[b, h, d, position]: one workgroup per (64 output positions
 // aligned to 64, head, batch). Position P holds token vt_slot(P) - dst_offset; LDS rows are
 // padded by 8 elements (272 bytes) so the column reads of the second phase spread over banks.
-__global__ __launch_bounds__(256) void v_heads_t_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst,
-                                                        long n_src, long n_dst, int heads, long dst_offset,
-                                                        long row_stride, long col_offset) {
-  __shared__ bf16 tile[64][136];
-  const long p0 = (dst_offset / 64 + blockIdx.x) * 64;  // first output position of the block
-  const long t0 = p0 - dst_offset;                       // token of position p0 (may be < 0)
-  const int head = blockIdx.y;
-  const long b = blockIdx.z;
+// Workgroup (position block `pblock`, head, batch b); every thread of the workgroup takes part.
+__device__ __forceinline__ void v_heads_t_block(const bf16* __restrict__ src, bf16* __restrict__ dst, long n_src,
+                                                long n_dst, int heads, long dst_offset, long row_stride,
+                                                long col_offset, long pblock, int head, long b,
+                                                bf16 (*tile)[136]) {
+  const long p0 = (dst_offset / 64 + pblock) * 64;  // first output position of the block
+  const long t0 = p0 - dst_offset;                   // token of position p0 (may be < 0)
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -255,6 +265,44 @@ __global__ __launch_bounds__(256) void v_heads_t_kernel(const bf16* __restrict__
         if (t0 + slot >= 0 && t0 + slot < n_src) o[e] = v[e];
       }
     }
+  }
+}
+
+__global__ __launch_bounds__(256) void v_heads_t_kernel(const bf16* __restrict__ src, bf16* __restrict__ dst,
+                                                        long n_src, long n_dst, int heads, long dst_offset,
+                                                        long row_stride, long col_offset) {
+  __shared__ bf16 tile[64][136];
+  v_heads_t_block(src, dst, n_src, n_dst, heads, dst_offset, row_stride, col_offset, blockIdx.x, blockIdx.y,
+                  blockIdx.z, tile);
+}
+
+// Q and K per-head RMSNorm + RoPE and the V^T transpose of one projection in one launch:
+// workgroups [0, q_blocks) run qk_norm_rope on the Q heads, [q_blocks, q_blocks + k_blocks) on
+// the K heads, the rest transpose the V heads (position block major, then head).
+struct QkvPrepareArgs {
+  const bf16* src;
+  bf16 *q, *k, *vt;
+  const float *q_weight, *k_weight, *cos_table, *sin_table;
+  long n_src, n_dst, n_vt, dst_offset, row_stride, q_col, k_col, v_col;
+  int heads, kv_heads;
+  long q_blocks, k_blocks, v_pos_blocks;
+  float eps;
+};
+
+__global__ __launch_bounds__(256) void qkv_prepare_kernel(QkvPrepareArgs a) {
+  __shared__ bf16 tile[64][136];
+  const long bx = blockIdx.x;
+  const long b = blockIdx.y;
+  if (bx < a.q_blocks) {
+    qk_norm_rope_block<bf16, bf16>(a.src, a.q, a.q_weight, a.cos_table, a.sin_table, a.n_src, a.n_dst, a.heads,
+                                   a.dst_offset, a.row_stride, a.q_col, a.eps, bx, b);
+  } else if (bx < a.q_blocks + a.k_blocks) {
+    qk_norm_rope_block<bf16, bf16>(a.src, a.k, a.k_weight, a.cos_table, a.sin_table, a.n_src, a.n_dst, a.kv_heads,
+                                   a.dst_offset, a.row_stride, a.k_col, a.eps, bx - a.q_blocks, b);
+  } else {
+    const long v = bx - a.q_blocks - a.k_blocks;
+    v_heads_t_block(a.src, a.vt, a.n_src, a.n_vt, a.kv_heads, a.dst_offset, a.row_stride, a.v_col,
+                    v % a.v_pos_blocks, static_cast<int>(v / a.v_pos_blocks), b, tile);
   }
 }
 
@@ -506,6 +554,36 @@ extern "C" int iris_v_heads_t(const void* src, void* dst, int batch, long n_src,
   v_heads_t_kernel<<<grid, 256, 0, stream>>>((const bf16*)src, (bf16*)dst, n_src, n_dst, heads, dst_offset,
                                              row_stride, col_offset);
   return check_launch("v_heads_t");
+}
+
+extern "C" int iris_qkv_prepare(const void* src, void* q, void* k, void* vt, const float* q_weight,
+                                const float* k_weight, const float* cos_table, const float* sin_table,
+                                long table_rows, int batch, long n_src, long n_dst, long n_vt, int heads,
+                                int kv_heads, long dst_offset, long row_stride, long q_col, long k_col, long v_col,
+                                float eps, hipStream_t stream) {
+  IRIS_REQUIRE(heads > 0 && kv_heads > 0 && kv_heads <= 65535, "qkv_prepare: bad head counts");
+  IRIS_REQUIRE(batch >= 0 && batch <= 65535 && n_src >= 0, "qkv_prepare: bad sizes");
+  IRIS_REQUIRE(q_col >= 0 && k_col >= 0 && v_col >= 0 && q_col + heads * 128L <= row_stride &&
+                   k_col + kv_heads * 128L <= row_stride && v_col + kv_heads * 128L <= row_stride,
+               "qkv_prepare needs a contiguous [B, N, W] projection holding the Q, K and V heads");
+  IRIS_REQUIRE(row_stride % 8 == 0 && q_col % 8 == 0 && k_col % 8 == 0 && v_col % 8 == 0,
+               "qkv_prepare: rows must be 16-byte aligned");
+  IRIS_REQUIRE(dst_offset >= 0 && dst_offset + n_src <= table_rows && dst_offset + n_src <= n_dst &&
+                   dst_offset + n_src <= n_vt,
+               "qkv_prepare: rotary tables or outputs do not cover the written rows");
+  IRIS_REQUIRE(n_vt % 64 == 0, "qkv_prepare: the V^T rows must be a multiple of 64 positions");
+  IRIS_REQUIRE(src && q && k && vt && q_weight && k_weight && cos_table && sin_table, "qkv_prepare: null pointer");
+  if (batch == 0 || n_src == 0) return IRIS_OK;
+  QkvPrepareArgs a{static_cast<const bf16*>(src), static_cast<bf16*>(q), static_cast<bf16*>(k),
+                   static_cast<bf16*>(vt), q_weight, k_weight, cos_table, sin_table, n_src, n_dst, n_vt,
+                   dst_offset, row_stride, q_col, k_col, v_col, heads, kv_heads, 0, 0, 0, eps};
+  a.q_blocks = (n_src * ((heads + kQkRows - 1) / kQkRows) + 15) / 16;
+  a.k_blocks = (n_src * ((kv_heads + kQkRows - 1) / kQkRows) + 15) / 16;
+  a.v_pos_blocks = (dst_offset + n_src + 63) / 64 - dst_offset / 64;
+  const long blocks = a.q_blocks + a.k_blocks + a.v_pos_blocks * kv_heads;
+  IRIS_REQUIRE(blocks < (1L << 31), "qkv_prepare: too many rows");
+  qkv_prepare_kernel<<<dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(batch)), 256, 0, stream>>>(a);
+  return check_launch("qkv_prepare");
 }
 
 extern "C" int iris_silu_add_rows(const float* x, const float* t, long rows, long rows_per_batch, int width,

@@ -441,9 +441,8 @@ class HipIris:
         q, k, vt = ws["q"], ws["k"], ws["vt"]
         for proj, st, rows, off in ((py, "y", T, 0), (px, "x", Lp, T)):
             pv = proj.view(B, rows, qkvg_w)
-            K.qk_norm_rope(pv, blk[f"q_norm_{st}"], rope_c, rope_s, eps, H, 0, out=q, offset=off)
-            K.qk_norm_rope(pv, blk[f"k_norm_{st}"], rope_c, rope_s, eps, Hkv, H * HEAD_DIM, out=k, offset=off)
-            K.v_heads_t(pv, Hkv, vt, (H + Hkv) * HEAD_DIM, off)
+            K.qkv_prepare(pv, blk[f"q_norm_{st}"], blk[f"k_norm_{st}"], rope_c, rope_s, eps, H, Hkv, q, k, vt,
+                          0, H * HEAD_DIM, (H + Hkv) * HEAD_DIM, off)
         gate_col = (H + 2 * Hkv) * HEAD_DIM
         K.flash_attention(q, k, vt, N, ay, ax, n_split=T, gate0=py[:, gate_col:], gate1=px[:, gate_col:])
         K.linear_grouped([ax, ay], [blk["proj_x_w"], blk["proj_y_w"]], [blk["proj_x_b"], blk["proj_y_b"]], [bx, by])
@@ -481,9 +480,8 @@ class HipIris:
         rope_c, rope_s = ws["rope"]
         pv = proj.view(B, N, qkvg_w)
         q, k, vt = ws["q"], ws["k"], ws["vt"]
-        K.qk_norm_rope(pv, blk["q_norm"], rope_c, rope_s, eps, H, 0, out=q, offset=0)
-        K.qk_norm_rope(pv, blk["k_norm"], rope_c, rope_s, eps, Hkv, H * HEAD_DIM, out=k, offset=0)
-        K.v_heads_t(pv, Hkv, vt, (H + Hkv) * HEAD_DIM, 0)
+        K.qkv_prepare(pv, blk["q_norm"], blk["k_norm"], rope_c, rope_s, eps, H, Hkv, q, k, vt,
+                      0, H * HEAD_DIM, (H + Hkv) * HEAD_DIM)
         gate = proj[:, (H + 2 * Hkv) * HEAD_DIM:]
         if not last:
             R, M, per_batch = tok, rows, N
@@ -521,9 +519,8 @@ class HipIris:
         K.linear(ws["cp"], blk["qkv_w"], out=ws["pq"])
         rope_c, rope_s = ws["rope_pix"]
         pv = ws["pq"].view(B, Lp, 3 * width)
-        K.qk_norm_rope(pv, blk["q_norm"], rope_c, rope_s, eps, heads, 0, out=ws["qp"])
-        K.qk_norm_rope(pv, blk["k_norm"], rope_c, rope_s, eps, heads, width, out=ws["kp"])
-        K.v_heads_t(pv, heads, ws["vtp"], 2 * width, 0)
+        K.qkv_prepare(pv, blk["q_norm"], blk["k_norm"], rope_c, rope_s, eps, heads, heads, ws["qp"], ws["kp"],
+                      ws["vtp"], 0, width, 2 * width)
         K.flash_attention(ws["qp"], ws["kp"], ws["vtp"], Lp, None, ws["pa"], n_split=0)
         K.linear(ws["pa"], blk["proj_w"], blk["proj_b"], out=ws["pr"])
         K.linear(ws["pr"], blk["expand_w"], blk["expand_b"], out=ws["ex"])
@@ -657,9 +654,7 @@ class HipIris:
         for i, blk in enumerate(self.text_blocks):
             K.linear(hy, blk["qkv_w"], blk["qkv_b"], out=qkv)
             pv = qkv.view(B, n, 3 * D)
-            K.qk_norm_rope(pv, blk["q_norm"], cos, sin, eps, H, 0, out=q)
-            K.qk_norm_rope(pv, blk["k_norm"], cos, sin, eps, H, D, out=k)
-            K.v_heads_t(pv, H, vt, 2 * D, 0)
+            K.qkv_prepare(pv, blk["q_norm"], blk["k_norm"], cos, sin, eps, H, H, q, k, vt, 0, D, 2 * D)
             K.flash_attention_masked(q, k, vt, n, ws["kmask"], att)
             K.linear(att, blk["proj_w"], blk["proj_b"], out=br)
             K.residual_rms_norm(Y, br, blk["norm2"], eps, hy)

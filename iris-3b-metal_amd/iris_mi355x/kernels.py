@@ -265,6 +265,45 @@ def v_heads_t(x: torch.Tensor, heads: int, out: torch.Tensor, col_offset: int = 
     return out
 
 
+def qkv_prepare(
+    x: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float,
+    heads: int,
+    kv_heads: int,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    vt: torch.Tensor,
+    q_col: int,
+    k_col: int,
+    v_col: int,
+    offset: int = 0,
+) -> None:
+    """``qk_norm_rope`` of the Q heads and of the K heads and ``v_heads_t`` of the V heads of one
+    BF16 ``[B, N, W]`` projection in one launch (same results as the three calls); ``q``:
+    ``[B, heads, N_out, 128]``, ``k``: ``[B, kv_heads, N_out, 128]``, ``vt``:
+    ``[B, kv_heads, 128, N_pad]``, all BF16, rows / positions from ``offset``."""
+    batch, tokens, width = x.shape
+    _on_gpu(x, q, k, vt, q_weight, k_weight, cos, sin)
+    _require(all(t.dtype == torch.bfloat16 for t in (x, q, k, vt)), "qkv_prepare works on BF16")
+    _require(x.is_contiguous() and q.is_contiguous() and k.is_contiguous() and vt.is_contiguous(),
+             "qkv_prepare needs contiguous tensors")
+    _require(q.shape == (batch, heads, q.shape[2], HEAD_DIM) and k.shape == (batch, kv_heads, q.shape[2], HEAD_DIM),
+             "qkv_prepare: q / k must be [B, heads, N, 128] buffers of equal length")
+    _require(vt.shape[:3] == (batch, kv_heads, HEAD_DIM), f"qkv_prepare: vt must be [{batch}, {kv_heads}, 128, N]")
+    _require(cos.shape == sin.shape == (cos.shape[0], HEAD_DIM // 2), "qkv_prepare: rotary tables must be [N, 64]")
+    _require_fp32(q_weight=q_weight, k_weight=k_weight, cos=cos, sin=sin)
+    _require(q_weight.numel() == HEAD_DIM and k_weight.numel() == HEAD_DIM, "qkv_prepare: gains have 128 entries")
+    L.call(
+        "iris_qkv_prepare", L.ptr(x), L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(q_weight), L.ptr(k_weight), L.ptr(cos),
+        L.ptr(sin), cos.shape[0], batch, tokens, q.shape[2], vt.shape[3], heads, kv_heads, offset, width, q_col,
+        k_col, v_col, float(eps), L.stream(),
+    )
+
+
 def linear(
     x: torch.Tensor,
     weight: torch.Tensor,

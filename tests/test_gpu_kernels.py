@@ -113,6 +113,36 @@ def test_qk_norm_rope_offsets_and_layout(src_dtype):
     assert torch.all(got[:, :, t + l:] == 0)
 
 
+@pytest.mark.parametrize("heads,kv_heads,n_text,n_image", [(20, 5, 256, 4096), (3, 3, 16, 48), (4, 1, 7, 90)])
+def test_qkv_prepare_is_the_three_calls(heads, kv_heads, n_text, n_image):
+    """One launch for Q / K norm + RoPE and the V transpose of a text and an image projection
+    (offsets 0 and n_text) gives bit for bit what qk_norm_rope, qk_norm_rope and v_heads_t write,
+    and leaves every other row and position as it was."""
+    b = 1 if n_image > 1000 else 2
+    g = torch.Generator(device=DEV).manual_seed(30)
+    width = (heads + 2 * kv_heads) * 128 + 256  # q | k | v | a gate-like tail
+    n = n_text + n_image
+    n_pad = (n + 63) // 64 * 64 + 64
+    cos = torch.randn(n_pad, 64, generator=g, device=DEV)
+    sin = torch.randn(n_pad, 64, generator=g, device=DEV)
+    wq = 1 + 0.1 * torch.randn(128, generator=g, device=DEV)
+    wk = 1 + 0.1 * torch.randn(128, generator=g, device=DEV)
+    projs = [torch.randn(b, rows, width, generator=g, device=DEV).to(torch.bfloat16) for rows in (n_text, n_image)]
+    bufs = [[torch.full(shape, 3.0, device=DEV, dtype=torch.bfloat16)
+             for shape in ((b, heads, n_pad, 128), (b, kv_heads, n_pad, 128), (b, kv_heads, 128, n_pad))]
+            for _ in range(2)]
+    k_col, v_col = heads * 128, (heads + kv_heads) * 128
+    for proj, off in zip(projs, (0, n_text)):
+        q1, k1, vt1 = bufs[0]
+        K.qk_norm_rope(proj, wq, cos, sin, 1e-6, heads, 0, out=q1, offset=off)
+        K.qk_norm_rope(proj, wk, cos, sin, 1e-6, kv_heads, k_col, out=k1, offset=off)
+        K.v_heads_t(proj, kv_heads, vt1, v_col, off)
+        K.qkv_prepare(proj, wq, wk, cos, sin, 1e-6, heads, kv_heads, *bufs[1], 0, k_col, v_col, off)
+    for one, fused in zip(*bufs):
+        assert torch.equal(one, fused)
+    assert torch.all(bufs[1][0][:, :, n:] == 3.0) and torch.all(bufs[1][1][:, :, n:] == 3.0)
+
+
 def test_qk_norm_rope_rejects_uncovered_rows():
     x = torch.randn(1, 10, 256, device=DEV)
     w = torch.ones(128, device=DEV)

@@ -47,7 +47,7 @@ def test_binding_covers_the_header():
 def test_abi_version(lib):
     from iris_mi355x import _lib
 
-    assert lib.iris_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.iris_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_build_recipe_targets_gfx950_without_packed_fp32():
