@@ -8,7 +8,7 @@ import torch
 
 from iris_mi355x.config import IRIS_3B, RELEASED_TOPOLOGY
 from iris_mi355x.engine import HipIris
-from iris_mi355x.sampling import turbo_sample
+from iris_mi355x.sampling import dpm1_sample, turbo_sample
 from iris_mi355x.weights import synthetic_state_dict
 from oracle import iris_oracle as O
 
@@ -188,6 +188,48 @@ def test_iris3b_encode_text_matches_oracle(iris3b_blocks):
     got = engine.encode_text(states.to(DEV), mask.to(DEV))
     check(got, want, "iris3b encode_text")
     check(got[:, :123], want[:, :123], "iris3b encode_text real tokens")
+
+
+@pytest.fixture(scope="module")
+def iris3b_full():
+    """Full-depth Iris-3B (8 dual + 16 single blocks, 4 PiT blocks) with seeded weights drawn on the GPU."""
+    return HipIris(IRIS_3B, synthetic_state_dict(IRIS_3B, seed=0, device=DEV), device=DEV)
+
+
+def test_iris3b_full_size_batch_of_four_is_four_single_forwards(iris3b_full):
+    """The guided workload's shape at full size (1024x1024, 4352 joint tokens, PiT over 1M pixels
+    per image, batch 4 = two prompts with conditional and zero unconditional text), checked by a
+    property the CPU oracle cannot reach at this size in seconds: every row of the batched
+    forward equals, bit for bit, the forward of that row alone (no kernel mixes rows, and every
+    output element accumulates over K in the same order whatever the launch shape)."""
+    engine = iris3b_full
+    g = torch.Generator(device=DEV).manual_seed(40)
+    x = torch.randn(4, 3, 1024, 1024, generator=g, device=DEV)
+    t = torch.tensor([700.0, 700.0, 250.0, 250.0], device=DEV)
+    cond = torch.randn(2, 256, IRIS_3B.hidden_size, generator=g, device=DEV)
+    text = torch.cat([cond, torch.zeros_like(cond)])
+    batched = engine(x, t, text).clone()
+    assert torch.isfinite(batched).all() and batched.abs().max() > 0
+    for i in range(4):
+        single = engine(x[i:i + 1], t[i:i + 1], text[i:i + 1])
+        assert torch.equal(single, batched[i:i + 1]), f"row {i}"
+
+
+def test_iris3b_full_size_guided_euler_with_equal_texts_is_unguided(iris3b_full):
+    """20 first-order steps at 1024x1024 with guidance 3.0 over two prompts (a batch of four
+    forwards per guided step): with the unconditional text equal to the conditional one the
+    guided trajectory is the unguided one bit for bit (u + 3 (c - u) = c when the two halves of
+    the batch agree); with zero unconditional text it leaves it and stays finite."""
+    engine = iris3b_full
+    g = torch.Generator(device=DEV).manual_seed(41)
+    z = torch.randn(2, 3, 1024, 1024, generator=g, device=DEV)
+    cond = torch.randn(2, 256, IRIS_3B.hidden_size, generator=g, device=DEV)
+    plain = dpm1_sample(engine, z, cond, None, steps=20).clone()
+    same = dpm1_sample(engine, z, cond, cond.clone(), steps=20, cfg_scale=3.0).clone()
+    assert torch.equal(plain, same)
+    guided = dpm1_sample(engine, z, cond, torch.zeros_like(cond), steps=20, cfg_scale=3.0)
+    assert torch.isfinite(guided).all()
+    assert not torch.equal(guided, plain)
 
 
 def test_graph_replays_match_eager_forward(released):
