@@ -101,18 +101,22 @@ __device__ __forceinline__ void store_row(const AttnArgs& p, const f32x16 (&o)[4
 // MASKED: query q attends key j < n iff key_mask[b, j] != 0 or j == q. A tile can then hold no
 // key of some query; its running max stays -inf and the exponentials use 0 in its place, so
 // they are exactly 0 instead of NaN.
-template <int QB, int STAGES, int KVT, bool STAGED, bool MASKED = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2 : 1))) void flash_attn_kernel(
-    AttnArgs p) {  // 32-row waves: two workgroups per CU (<= 256 registers per lane)
+// NW: waves per workgroup; with NW = 12 (one workgroup per CU, three waves per SIMD: four query
+// heads x three 32-row blocks) the first four waves fetch the K/V tiles that all twelve share,
+// a third of the fetches of three 4-wave workgroups (global_load_lds ring only).
+template <int QB, int STAGES, int KVT, bool STAGED, bool MASKED = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 12 ? 3 : (QB == 1 ? 2 : 1)))) void
+flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
   constexpr int KB = KVT / 32;     // 32-key blocks per tile
   constexpr int TILE = KVT * kHd;  // elements of one K (or V^T) tile
   constexpr int STAGE = 2 * TILE;  // K tile then V^T tile
-  constexpr int LOADS = KVT / 16;  // 1 KB loads per wave per operand per tile
+  constexpr int LOADS = KVT / 16;  // 1 KB loads per fetching wave per operand per tile
   constexpr int LPW = 2 * LOADS;
   constexpr int VCPR = KVT / 8;    // 16-byte chunks per V^T row
   constexpr int VRPL = 64 / VCPR;  // V^T rows per 1 KB load
   static_assert(KVT == 32 || KVT == 64, "K/V tile of 32 or 64 keys");
   static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64 && (!STAGED || STAGES == 2), "pipeline depth");
+  static_assert(NW == 4 || (NW == 12 && !STAGED), "twelve-wave workgroups use the global_load_lds ring");
   __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
   // logical workgroup: (b, kv head, head group) major, query block minor; the XCD remap keeps
@@ -158,6 +162,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
     v_off[j] = vd * static_cast<int>(n_pad) + 8 * ((lane % VCPR) ^ swz<VCPR>(vd));
   }
   auto issue = [&](int t, int stage) {
+    if (NW != 4 && w >= 4) return;  // (wave-uniform: the first four waves fetch)
     bf16* kl = lds + stage * STAGE;
     bf16* vl = kl + TILE;
     const bf16* kt = kh + static_cast<long>(t) * KVT * kHd;
@@ -373,13 +378,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QB == 1 ? 2
 struct Variant {
   int qb, stages, kvt;
   bool staged;
+  int nw = 4;
 };
 // 0: 32 query rows per wave, 64-key tiles staged through registers; 1: the same with 32-key
-// tiles; 2: 64-key tiles, 2-stage global_load_lds ring; 3: 32-key tiles, 3-stage ring.
-// (Measured and dropped: an eight-wave ping-pong of MFMA and softmax phases, 1.8x slower at the
+// tiles; 2: 64-key tiles, 2-stage global_load_lds ring; 3: 32-key tiles, 3-stage ring; 4: 32-key
+// tiles in a 3-stage ring shared by twelve waves (four query heads x three row blocks).
+// (Measured and dropped: twelve-wave rings of 4 and 6 stages (1-2% slower than 3), eight of the
+// twelve waves fetching instead of four (2% slower), 64-key tiles at twelve waves (spills); an eight-wave ping-pong of MFMA and softmax phases, 1.8x slower at the
 // trunk shape; a software-pipelined wave issuing tile t - 1's P.V MFMAs around tile t's softmax,
 // no faster than variant 1; 64- and 96-row waves at one wave per SIMD, 1.5-1.9x slower.)
-constexpr Variant kVariants[] = {{1, 2, 64, true}, {1, 2, 32, true}, {1, 2, 64, false}, {1, 3, 32, false}};
+constexpr Variant kVariants[] = {
+    {1, 2, 64, true}, {1, 2, 32, true}, {1, 2, 64, false}, {1, 3, 32, false}, {1, 3, 32, false, 12}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 int g_attn_variant = -1;
 
@@ -427,13 +436,24 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   args.n_pad = static_cast<int>(n_pad);
   args.n_split = static_cast<int>(n_split);
   args.hpw = group < 4 ? group : 4;
-  // Grouped heads (the trunk's 20 query / 5 K/V heads): 32-key tiles staged through registers
-  // (168 VGPRs, three workgroups per CU, so the 680 workgroups of a 4352-token batch run in
-  // one round); one query head per K/V head (the pixel stage): 64-key tiles in a global_load_lds
-  // ring. Both measured fastest at their shapes.
-  const int variant = g_attn_variant >= 0 ? g_attn_variant : (group >= 4 ? 1 : 2);
+  // Grouped heads (the trunk's 20 query / 5 K/V heads): twelve-wave workgroups sharing one K/V
+  // ring (one per CU; 230 of them cover a 4352-token sequence) when their rounds over the CUs
+  // are at least 80% full, 9-11% faster than variant 1 there; else 32-key tiles staged through
+  // registers in three 4-wave workgroups per CU (variant 1: 168 VGPRs; small grids spread
+  // over more CUs). One query head per K/V head (the pixel stage): 64-key tiles in a
+  // global_load_lds ring. Each measured fastest at its shapes.
+  int variant = g_attn_variant;
+  if (variant < 0) {
+    variant = group >= 4 ? 1 : 2;
+    if (group >= 4) {
+      const int cus = device_cus();
+      const long wide = static_cast<long>(batch) * kv_heads * (group / 4) * ((n + 95) / 96);
+      const long rounds = (wide + cus - 1) / cus;
+      if (wide >= 0.8 * rounds * cus) variant = 4;
+    }
+  }
   const Variant v = kVariants[variant];
-  args.rows_per_wg = 32 * v.qb * 4 / args.hpw;
+  args.rows_per_wg = 32 * v.qb * v.nw / args.hpw;
   args.n_qblocks = static_cast<int>((n + args.rows_per_wg - 1) / args.rows_per_wg);
   args.n_hgroups = group / args.hpw;
   const long total = static_cast<long>(batch) * kv_heads * args.n_hgroups * args.n_qblocks;
@@ -451,8 +471,11 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
     case 2:
       flash_attn_kernel<1, 2, 64, false><<<grid, 256, 0, stream>>>(args);
       break;
-    default:
+    case 3:
       flash_attn_kernel<1, 3, 32, false><<<grid, 256, 0, stream>>>(args);
+      break;
+    default:
+      flash_attn_kernel<1, 3, 32, false, false, 12><<<grid, dim3(768), 0, stream>>>(args);
       break;
   }
   return check_launch("flash_attn");

@@ -663,19 +663,6 @@ int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   return check_launch("gemm_bf16");
 }
 
-// Compute units of the current device (the persistent kernels launch one workgroup per CU).
-int device_cus() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    cached[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0
-                      ? cus
-                      : 256;
-  }
-  return cached[dev];
-}
 
 // Plain BF16 output runs persistently (one workgroup per CU, the next tile's first K tile
 // loaded while the current tile is stored); the SwiGLU and FP32 epilogues keep one tile per

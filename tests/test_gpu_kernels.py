@@ -248,7 +248,7 @@ def _attn_inputs(b, h, hkv, n, seed):
 
 
 @pytest.mark.parametrize("n", [333, 352])
-@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
 def test_flash_attention_variants(variant, n):
     b, h, hkv = 1, 8, 2
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 16)
@@ -272,7 +272,7 @@ def test_flash_attention_small(b, h, hkv, n):
     close_bf16(out.view(b, n, -1), want, scale=1.0, floor=4e-3)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
 def test_flash_attention_rows_do_not_depend_on_padding_rows(variant):
     """A query row's output is bit-identical whatever the padding query rows (>= n) hold: the
     lazy max raise is decided per column, not per wave."""
