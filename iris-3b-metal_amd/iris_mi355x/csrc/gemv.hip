@@ -8,7 +8,7 @@ namespace iris {
 namespace {
 
 constexpr int kMaxBatch = 4;
-constexpr int kRowsPerWave = 4;
+constexpr int kRowsPerWave = 2;
 constexpr int kRowsPerBlock = 4 * kRowsPerWave;
 
 __global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ w, const float* __restrict__ x,
@@ -46,15 +46,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ w, c
 #pragma unroll
     for (int b = 0; b < kMaxBatch; ++b) {
       if (b >= nb) break;
-      float y = wave_sum(acc[b]);
-      if (lane == 0) {
-        if (bias) y += bias[row];
-        if (out_act == IRIS_ACT_SILU) y = silu(y);
-        if (n_extra == 0) {
-          out[b * out_bstride + row] = y;
-        } else {
-          for (int j = 0; j < n_extra; ++j) out[j * out_jstride + b * out_bstride + row] = y + extra[static_cast<long>(j) * n + row];
-        }
+      float y = wave_sum(acc[b]);  // (every lane holds the sum)
+      if (bias) y += bias[row];
+      if (out_act == IRIS_ACT_SILU) y = silu(y);
+      if (n_extra == 0) {
+        if (lane == 0) out[b * out_bstride + row] = y;
+      } else {  // the per-block copies, one per lane
+        for (int j = lane; j < n_extra; j += kWave)
+          out[j * out_jstride + b * out_bstride + row] = y + extra[static_cast<long>(j) * n + row];
       }
     }
   }

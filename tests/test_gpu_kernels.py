@@ -427,8 +427,10 @@ def test_residual_rms_norm_with_position_rows(branch_dtype):
 
 
 # -- conditioning, pixel stage, sampler ----------------------------------------------------
-def test_gemv_with_core_biases():
-    n, k, j, b = 1536, 256, 3, 2
+@pytest.mark.parametrize("j", [3, 24, 70])
+def test_gemv_with_core_biases(j):
+    """The shared adaLN core plus one bias row per block (24 in Iris-3B; 70 > one wave of lanes)."""
+    n, k, b = 1536, 256, 2
     g = gen(11)
     w = (0.05 * torch.randn(n, k, generator=g)).to(torch.bfloat16)
     x = torch.randn(b, k, generator=g)
