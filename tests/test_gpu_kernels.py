@@ -262,6 +262,25 @@ def test_flash_attention_variants(variant, n):
     close_bf16(out.view(b, n, -1), want, scale=1.0, floor=4e-3)
 
 
+@pytest.mark.parametrize("n", [77, 4352])
+def test_flash_attention_32_key_variants_agree_bitwise(n):
+    """The variants with 32-key tiles (register-staged, 3-stage ring, twelve-wave shared ring)
+    differ only in how K/V reach LDS: the same products and sums in the same order, so the same
+    bits; the automatic choice between them (by grid size) keeps batched and single runs equal."""
+    b, h, hkv = 1, 20, 5
+    q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 19)
+    outs = []
+    try:
+        for variant in (1, 3, 4):
+            _lib.call("iris_flash_attn_force_variant", variant)
+            out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+            K.flash_attention(qd, kd, vt, n, None, out, n_split=0)
+            outs.append(out)
+    finally:
+        _lib.call("iris_flash_attn_force_variant", -1)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 @pytest.mark.parametrize("b,h,hkv,n", [(1, 2, 1, 52), (2, 4, 1, 200), (1, 8, 2, 130), (1, 2, 2, 300)])
 def test_flash_attention_small(b, h, hkv, n):
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 8)
