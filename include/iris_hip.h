@@ -58,6 +58,18 @@ int iris_gated_residual_norm_modulate(float* residual, const void* branch, int b
                                       const float* next_scale, long next_mod_stride, void* next_out,
                                       int next_out_dtype, hipStream_t stream);
 
+/* The image- and text-stream calls of a dual-stream block in one launch (no reference
+ * counterpart; the reference calls gated_residual_rms_norm_ once per stream,
+ * model.py:286-289, 311-313): group i is iris_gated_residual_rms_norm (next_out == NULL) or
+ * iris_gated_residual_norm_modulate on its own tensors, with the same results; groups = 1 or 2,
+ * one branch dtype, one width, one next_out dtype. */
+int iris_gated_residual_grouped(int groups, float* const* residual, const void* const* branch, int branch_dtype,
+                                const float* const* weight, const float* const* gate, const long* rows,
+                                const long* rows_per_batch, int width, const long* mod_stride, float eps,
+                                const float* const* next_weight, const float* const* next_shift,
+                                const float* const* next_scale, const long* next_mod_stride, void* const* next_out,
+                                int next_out_dtype, hipStream_t stream);
+
 /* qk_norm_rope (src/iris_metal/kernels.py:37-84, wrapper 334-397): per (batch, token, head)
  * RMSNorm over 128 values with an FP32 gain, then rotation of pairs (2j, 2j+1) by
  * (cos, sin)[dst_offset + token, j]; reads heads at col_offset of a [batch, n_src, row_stride]

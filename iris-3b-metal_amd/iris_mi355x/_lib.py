@@ -28,6 +28,7 @@ _SIGNATURES: dict[str, list] = {
     "iris_gated_residual_rms_norm": [P, P, c_int, P, P, c_long, c_long, c_int, c_long, c_float, P],
     "iris_gated_residual_norm_modulate": [P, P, c_int, P, P, c_long, c_long, c_int, c_long, c_float, P, P, P,
                                           c_long, P, c_int, P],
+    "iris_gated_residual_grouped": [c_int, P, P, c_int, P, P, P, P, c_int, P, c_float, P, P, P, P, P, c_int, P],
     "iris_qk_norm_rope": [P, c_int, P, c_int, P, P, P, c_long, c_int, c_long, c_long, c_int, c_long, c_long,
                           c_long, c_float, P],
     "iris_v_heads_t": [P, P, c_int, c_long, c_long, c_int, c_long, c_long, c_long, P],
@@ -124,3 +125,7 @@ def pointer_array(values) -> ctypes.Array:
 
 def int_array(values) -> ctypes.Array:
     return (c_int * len(values))(*values)
+
+
+def long_array(values) -> ctypes.Array:
+    return (c_long * len(values))(*values)

@@ -84,13 +84,44 @@ __global__ __launch_bounds__(256) void rms_norm_modulate_kernel(const TI* __rest
 // updated row still in registers (the next branch's input norm, without re-reading the row).
 // Coefficients (gate * weight, and next_weight * (1 + next_scale), next_shift) are held per
 // wave as in rms_norm_modulate_kernel.
+// One launch serves up to two groups of rows with their own tensors (the image and text streams
+// of a dual-stream block): workgroups [0, blocks0) take group 0, the rest group 1.
+struct GatedGroup {
+  float* residual;
+  const void* branch;
+  const float* weight;
+  const float* gate;
+  long rows, rows_per_batch, mod_stride;
+  const float* next_weight;
+  const float* next_shift;
+  const float* next_scale;
+  long next_mod_stride;
+  void* next_out;
+};
+struct GatedArgs {
+  GatedGroup g[2];
+  long blocks0;
+  int width;
+  float eps;
+};
+
 template <int NC, typename TB, typename TO>
-__global__ __launch_bounds__(256) void gated_residual_kernel(
-    float* __restrict__ residual, const TB* __restrict__ branch, const float* __restrict__ weight,
-    const float* __restrict__ gate, long rows, long rows_per_batch, int width, long mod_stride, float eps,
-    const float* __restrict__ next_weight, const float* __restrict__ next_shift,
-    const float* __restrict__ next_scale, long next_mod_stride, TO* __restrict__ next_out) {
-  const long row = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+__global__ __launch_bounds__(256) void gated_residual_kernel(GatedArgs a) {
+  const bool second = blockIdx.x >= a.blocks0;
+  const GatedGroup& gg = second ? a.g[1] : a.g[0];
+  float* __restrict__ residual = gg.residual;
+  const TB* __restrict__ branch = static_cast<const TB*>(gg.branch);
+  const float* __restrict__ weight = gg.weight;
+  const float* __restrict__ gate = gg.gate;
+  const long rows = gg.rows, rows_per_batch = gg.rows_per_batch, mod_stride = gg.mod_stride;
+  const float* __restrict__ next_weight = gg.next_weight;
+  const float* __restrict__ next_shift = gg.next_shift;
+  const float* __restrict__ next_scale = gg.next_scale;
+  const long next_mod_stride = gg.next_mod_stride;
+  TO* __restrict__ next_out = static_cast<TO*>(gg.next_out);
+  const int width = a.width;
+  const float eps = a.eps;
+  const long row = (static_cast<long>(blockIdx.x) - (second ? a.blocks0 : 0)) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int nc = width >> 3;
@@ -414,44 +445,63 @@ int nc_bucket(int width) {
 bool valid_dtype(int dt) { return dt == IRIS_F32 || dt == IRIS_BF16; }
 
 template <int NC, typename TB>
-void launch_gated(dim3 grid, hipStream_t stream, float* residual, const void* branch, const float* weight,
-                  const float* gate, long rows, long rows_per_batch, int width, long mod_stride, float eps,
-                  const float* nw, const float* nsh, const float* nsc, long nstride, void* next_out, int out_dtype) {
+void launch_gated(dim3 grid, hipStream_t stream, const GatedArgs& a, int out_dtype) {
   if (out_dtype == IRIS_F32)
-    gated_residual_kernel<NC, TB, float><<<grid, 256, 0, stream>>>(residual, (const TB*)branch, weight, gate, rows,
-                                                                   rows_per_batch, width, mod_stride, eps, nw, nsh,
-                                                                   nsc, nstride, (float*)next_out);
+    gated_residual_kernel<NC, TB, float><<<grid, 256, 0, stream>>>(a);
   else
-    gated_residual_kernel<NC, TB, bf16><<<grid, 256, 0, stream>>>(residual, (const TB*)branch, weight, gate, rows,
-                                                                  rows_per_batch, width, mod_stride, eps, nw, nsh,
-                                                                  nsc, nstride, (bf16*)next_out);
+    gated_residual_kernel<NC, TB, bf16><<<grid, 256, 0, stream>>>(a);
+}
+
+int check_group(const GatedGroup& g) {
+  IRIS_REQUIRE(g.rows >= 0 && g.rows_per_batch > 0, "gated_residual_rms_norm: bad row counts");
+  IRIS_REQUIRE(g.mod_stride % 4 == 0 && aligned(g.gate, 16) && aligned(g.weight, 16),
+               "gated_residual_rms_norm: gate rows must be 16-byte aligned");
+  IRIS_REQUIRE(g.residual && g.branch && g.weight && g.gate, "gated_residual_rms_norm: null pointer");
+  IRIS_REQUIRE(!g.next_out || (g.next_weight && g.next_shift && g.next_scale && g.next_mod_stride % 4 == 0 &&
+                               aligned(g.next_weight, 16) && aligned(g.next_shift, 16) && aligned(g.next_scale, 16)),
+               "gated_residual_rms_norm: the next norm needs 16-byte aligned FP32 gain and modulation rows");
+  return IRIS_OK;
+}
+
+// groups: 1 or 2 entries of g; both with or both without the next norm.
+int gated_launch(int groups, const GatedGroup* g, int branch_dtype, int width, float eps, int out_dtype,
+                 hipStream_t stream) {
+  IRIS_REQUIRE(valid_dtype(branch_dtype) && valid_dtype(out_dtype), "gated_residual_rms_norm: unknown dtype");
+  IRIS_REQUIRE(width > 0 && width % 128 == 0 && width <= 8192,
+               "gated_residual_rms_norm_ shape mismatch: width %% 128 == 0 and <= 8192 (got %d)", width);
+  GatedArgs a{};
+  long blocks = 0;
+  for (int i = 0; i < groups; ++i) {
+    const int rc = check_group(g[i]);
+    if (rc) return rc;
+    IRIS_REQUIRE((g[i].next_out == nullptr) == (g[0].next_out == nullptr),
+                 "gated_residual_rms_norm: both groups with or both without the next norm");
+    a.g[i] = g[i];
+    const long b = (g[i].rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (i == 0) a.blocks0 = b;
+    blocks += b;
+  }
+  if (groups == 1) a.g[1] = a.g[0];
+  a.width = width;
+  a.eps = eps;
+  if (blocks == 0) return IRIS_OK;
+  IRIS_REQUIRE(blocks < (1L << 31), "gated_residual_rms_norm: too many rows");
+  const dim3 grid(static_cast<unsigned>(blocks));
+  IRIS_NC_DISPATCH(nc_bucket(width), {
+    if (branch_dtype == IRIS_BF16)
+      launch_gated<NC, bf16>(grid, stream, a, out_dtype);
+    else
+      launch_gated<NC, float>(grid, stream, a, out_dtype);
+  })
+  return check_launch("gated_residual_rms_norm");
 }
 
 int gated_common(float* residual, const void* branch, int branch_dtype, const float* weight, const float* gate,
                  long rows, long rows_per_batch, int width, long mod_stride, float eps, const float* nw,
                  const float* nsh, const float* nsc, long nstride, void* next_out, int out_dtype,
                  hipStream_t stream) {
-  IRIS_REQUIRE(valid_dtype(branch_dtype) && valid_dtype(out_dtype), "gated_residual_rms_norm: unknown dtype");
-  IRIS_REQUIRE(width > 0 && width % 128 == 0 && width <= 8192,
-               "gated_residual_rms_norm_ shape mismatch: width %% 128 == 0 and <= 8192 (got %d)", width);
-  IRIS_REQUIRE(rows >= 0 && rows_per_batch > 0, "gated_residual_rms_norm: bad row counts");
-  IRIS_REQUIRE(mod_stride % 4 == 0 && aligned(gate, 16) && aligned(weight, 16),
-               "gated_residual_rms_norm: gate rows must be 16-byte aligned");
-  IRIS_REQUIRE(residual && branch && weight && gate, "gated_residual_rms_norm: null pointer");
-  IRIS_REQUIRE(!next_out || (nw && nsh && nsc && nstride % 4 == 0 && aligned(nw, 16) && aligned(nsh, 16) &&
-                             aligned(nsc, 16)),
-               "gated_residual_rms_norm: the next norm needs 16-byte aligned FP32 gain and modulation rows");
-  if (rows == 0) return IRIS_OK;
-  const dim3 grid(static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
-  IRIS_NC_DISPATCH(nc_bucket(width), {
-    if (branch_dtype == IRIS_BF16)
-      launch_gated<NC, bf16>(grid, stream, residual, branch, weight, gate, rows, rows_per_batch, width, mod_stride,
-                             eps, nw, nsh, nsc, nstride, next_out, out_dtype);
-    else
-      launch_gated<NC, float>(grid, stream, residual, branch, weight, gate, rows, rows_per_batch, width,
-                              mod_stride, eps, nw, nsh, nsc, nstride, next_out, out_dtype);
-  })
-  return check_launch("gated_residual_rms_norm");
+  const GatedGroup g{residual, branch, weight, gate, rows, rows_per_batch, mod_stride, nw, nsh, nsc, nstride, next_out};
+  return gated_launch(1, &g, branch_dtype, width, eps, out_dtype, stream);
 }
 
 }  // namespace
@@ -504,6 +554,29 @@ extern "C" int iris_gated_residual_norm_modulate(float* residual, const void* br
   IRIS_REQUIRE(next_out != nullptr, "gated_residual_norm_modulate: next_out is required");
   return gated_common(residual, branch, branch_dtype, weight, gate, rows, rows_per_batch, width, mod_stride, eps,
                       next_weight, next_shift, next_scale, next_mod_stride, next_out, next_out_dtype, stream);
+}
+
+extern "C" int iris_gated_residual_grouped(int groups, float* const* residual, const void* const* branch,
+                                           int branch_dtype, const float* const* weight, const float* const* gate,
+                                           const long* rows, const long* rows_per_batch, int width,
+                                           const long* mod_stride, float eps, const float* const* next_weight,
+                                           const float* const* next_shift, const float* const* next_scale,
+                                           const long* next_mod_stride, void* const* next_out, int next_out_dtype,
+                                           hipStream_t stream) {
+  IRIS_REQUIRE(groups == 1 || groups == 2, "gated_residual_grouped: 1 or 2 groups");
+  IRIS_REQUIRE(residual && branch && weight && gate && rows && rows_per_batch && mod_stride,
+               "gated_residual_grouped: null array");
+  const bool next = next_out != nullptr;
+  IRIS_REQUIRE(!next || (next_weight && next_shift && next_scale && next_mod_stride),
+               "gated_residual_grouped: the next norm's arrays are missing");
+  GatedGroup g[2] = {};
+  for (int i = 0; i < groups; ++i) {
+    g[i] = GatedGroup{residual[i], branch[i], weight[i], gate[i], rows[i], rows_per_batch[i], mod_stride[i],
+                      next ? next_weight[i] : nullptr, next ? next_shift[i] : nullptr, next ? next_scale[i] : nullptr,
+                      next ? next_mod_stride[i] : 0, next ? next_out[i] : nullptr};
+    IRIS_REQUIRE(!next || g[i].next_out, "gated_residual_grouped: next_out %d is null", i);
+  }
+  return gated_launch(groups, g, branch_dtype, width, eps, next ? next_out_dtype : IRIS_BF16, stream);
 }
 
 extern "C" int iris_qk_norm_rope(const void* src, int src_dtype, void* dst, int dst_dtype, const float* weight,

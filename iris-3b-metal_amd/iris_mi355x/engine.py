@@ -446,22 +446,22 @@ class HipIris:
         gate_col = (H + 2 * Hkv) * HEAD_DIM
         K.flash_attention(q, k, vt, N, ay, ax, n_split=T, gate0=py[:, gate_col:], gate1=px[:, gate_col:])
         K.linear_grouped([ax, ay], [blk["proj_x_w"], blk["proj_y_w"]], [blk["proj_x_b"], blk["proj_y_b"]], [bx, by])
-        K.gated_residual_norm_modulate_(X, bx.view(B, Lp, D), blk["attn_post_norm_x"], xm[2], eps,
-                                        blk["norm_x2"], xm[3], xm[4], hx.view(B, Lp, D))
-        K.gated_residual_norm_modulate_(Y, by.view(B, T, D), blk["attn_post_norm_y"], ym[2], eps,
-                                        blk["norm_y2"], ym[3], ym[4], hy.view(B, T, D))
+        K.gated_residual_grouped_([X, Y], [bx.view(B, Lp, D), by.view(B, T, D)],
+                                  [blk["attn_post_norm_x"], blk["attn_post_norm_y"]], [xm[2], ym[2]], eps,
+                                  [blk["norm_x2"], blk["norm_y2"]], [xm[3], ym[3]], [xm[4], ym[4]],
+                                  [hx.view(B, Lp, D), hy.view(B, T, D)])
         K.linear_grouped([hx, hy], [blk["w13_x"], blk["w13_y"]], None, [hhx, hhy], swiglu=True)
         K.linear_grouped([hhx, hhy], [blk["w2_x"], blk["w2_y"]], None, [bx, by])
         if nxt is None:
-            K.gated_residual_rms_norm_(X, bx.view(B, Lp, D), blk["mlp_post_norm_x"], xm[5], eps)
-            K.gated_residual_rms_norm_(Y, by.view(B, T, D), blk["mlp_post_norm_y"], ym[5], eps)
+            K.gated_residual_grouped_([X, Y], [bx.view(B, Lp, D), by.view(B, T, D)],
+                                      [blk["mlp_post_norm_x"], blk["mlp_post_norm_y"]], [xm[5], ym[5]], eps)
         else:
             nx = [self._mods(ws, "mods_img", nxt["img_mod"], c) for c in range(2)]
             ny = [self._mods(ws, "mods_txt", nxt["txt_mod"], c) for c in range(2)]
-            K.gated_residual_norm_modulate_(X, bx.view(B, Lp, D), blk["mlp_post_norm_x"], xm[5], eps,
-                                            nxt["norm_x1"], nx[0], nx[1], hx.view(B, Lp, D))
-            K.gated_residual_norm_modulate_(Y, by.view(B, T, D), blk["mlp_post_norm_y"], ym[5], eps,
-                                            nxt["norm_y1"], ny[0], ny[1], hy.view(B, T, D))
+            K.gated_residual_grouped_([X, Y], [bx.view(B, Lp, D), by.view(B, T, D)],
+                                      [blk["mlp_post_norm_x"], blk["mlp_post_norm_y"]], [xm[5], ym[5]], eps,
+                                      [nxt["norm_x1"], nxt["norm_y1"]], [nx[0], ny[0]], [nx[1], ny[1]],
+                                      [hx.view(B, Lp, D), hy.view(B, T, D)])
 
     def _single_block(self, ws: dict, blk: dict, B: int, T: int, Lp: int, N: int, last: bool, h_ready: bool,
                       nxt: dict | None) -> None:

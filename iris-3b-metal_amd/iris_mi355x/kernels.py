@@ -170,6 +170,53 @@ def gated_residual_norm_modulate_(
     return out
 
 
+def gated_residual_grouped_(residuals, branches, weights, gates, eps: float, next_weights=None, next_shifts=None,
+                            next_scales=None, outs=None) -> None:
+    """``gated_residual_rms_norm_`` (``outs`` None) or ``gated_residual_norm_modulate_`` of two
+    streams (the image and text rows of a dual-stream block) in one launch, each on its own
+    tensors; same results as the two calls."""
+    _require(len(residuals) == len(branches) == len(weights) == len(gates) == 2, "gated_residual_grouped_ takes two")
+    nxt = outs is not None
+    width = residuals[0].shape[-1]
+    keep, rows, per_batch, strides, nstrides, shifts, scales = [], [], [], [], [], [], []
+    for i in range(2):
+        residual, branch = residuals[i], branches[i]
+        batch, tokens, w = residual.shape
+        _on_gpu(residual, branch, weights[i], gates[i])
+        _require(w == width and w % 128 == 0 and branch.shape == residual.shape and branch.is_contiguous(),
+                 "gated_residual_grouped_ shape mismatch")
+        _require(branch.dtype == branches[0].dtype, "gated_residual_grouped_: branch dtypes differ")
+        _require_fp32(residual=residual, weight=weights[i])
+        _require(weights[i].numel() == width, "gated_residual_grouped_ gain width mismatch")
+        gate, gate_stride = _per_batch(gates[i], batch, width)
+        keep.append(gate)
+        rows.append(batch * tokens)
+        per_batch.append(tokens)
+        strides.append(gate_stride)
+        if nxt:
+            _on_gpu(next_weights[i], next_shifts[i], next_scales[i], outs[i])
+            _require(outs[i].is_contiguous() and outs[i].shape == residual.shape and outs[i].dtype == outs[0].dtype,
+                     "gated_residual_grouped_: bad output")
+            _require_fp32(next_weight=next_weights[i])
+            shift, shift_stride = _per_batch(next_shifts[i], batch, width)
+            scale, scale_stride = _per_batch(next_scales[i], batch, width)
+            if shift_stride != scale_stride:
+                shift, scale = shift.contiguous(), scale.contiguous()
+                shift_stride = width
+            shifts.append(shift)
+            scales.append(scale)
+            nstrides.append(shift_stride)
+    P = L.pointer_array
+    L.call(
+        "iris_gated_residual_grouped", 2, P([L.ptr(r) for r in residuals]), P([L.ptr(b) for b in branches]),
+        L.dtype_code(branches[0].dtype), P([L.ptr(w) for w in weights]), P([L.ptr(g) for g in keep]),
+        L.long_array(rows), L.long_array(per_batch), width, L.long_array(strides), float(eps),
+        P([L.ptr(w) for w in next_weights]) if nxt else None, P([L.ptr(x) for x in shifts]) if nxt else None,
+        P([L.ptr(x) for x in scales]) if nxt else None, L.long_array(nstrides) if nxt else None,
+        P([L.ptr(o) for o in outs]) if nxt else None, L.dtype_code(outs[0].dtype) if nxt else L.BF16, L.stream(),
+    )
+
+
 def pixel_rms_norm(pixels: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """``rms_norm(pixels) * weight`` over the 16 channels of each pixel, stored BF16
     (src/iris_metal/kernels.py:486-498)."""

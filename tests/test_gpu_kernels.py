@@ -173,6 +173,40 @@ def test_v_heads_t_writes_the_permuted_transpose(offset, n):
     assert torch.all(got[..., ~inside] == 3.0)
 
 
+@pytest.mark.parametrize("with_next", [False, True])
+def test_gated_residual_grouped_is_the_two_calls(with_next):
+    """The image and text rows of a dual-stream block in one launch: bit for bit the two
+    separate calls, each group on its own residual, branch, gain, gate and next-norm tensors."""
+    g = torch.Generator(device=DEV).manual_seed(31)
+    b, d = 2, 2560
+    shapes = [(b, 1024, d), (b, 37, d)]
+    res = [torch.randn(s, generator=g, device=DEV) for s in shapes]
+    br = [torch.randn(s, generator=g, device=DEV).to(torch.bfloat16) for s in shapes]
+    w = [1 + 0.1 * torch.randn(d, generator=g, device=DEV) for _ in shapes]
+    mods = [0.1 * torch.randn(b, 1, 6 * d, generator=g, device=DEV) for _ in shapes]
+    gate = [m[..., :d] for m in mods]
+    nw = [1 + 0.1 * torch.randn(d, generator=g, device=DEV) for _ in shapes]
+    shift = [m[..., d:2 * d] for m in mods]
+    scale = [m[..., 2 * d:3 * d] for m in mods]
+    one = [r.clone() for r in res]
+    grouped = [r.clone() for r in res]
+    outs1 = [torch.empty(s, device=DEV, dtype=torch.bfloat16) for s in shapes]
+    outs2 = [torch.empty(s, device=DEV, dtype=torch.bfloat16) for s in shapes]
+    for i in range(2):
+        if with_next:
+            K.gated_residual_norm_modulate_(one[i], br[i], w[i], gate[i], 1e-6, nw[i], shift[i], scale[i], outs1[i])
+        else:
+            K.gated_residual_rms_norm_(one[i], br[i], w[i], gate[i], 1e-6)
+    if with_next:
+        K.gated_residual_grouped_(grouped, br, w, gate, 1e-6, nw, shift, scale, outs2)
+    else:
+        K.gated_residual_grouped_(grouped, br, w, gate, 1e-6)
+    for i in range(2):
+        assert torch.equal(one[i], grouped[i])
+        if with_next:
+            assert torch.equal(outs1[i], outs2[i])
+
+
 # -- GEMM --------------------------------------------------------------------------------
 def _gemm_ref(a, w, bias=None):
     out = a.float().cpu() @ w.float().cpu().T
