@@ -1,7 +1,7 @@
 """Kernel microbenchmarks of libiris_hip.so (one GPU), also used as rocprofv3 drivers.
 
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench fused-ops
-    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench gemm 4352 6400 2560
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench gemm 4352 6400 2560 [--swiglu] [--rotate 6]
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench attention 1 20 5 4352
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench copy 1
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench encode-text 1 200
@@ -120,18 +120,22 @@ def fused_ops(iters: int = 50) -> list[dict]:
     return results
 
 
-def gemm(m: int, n: int, k: int, tile: int = -1, iters: int = 20) -> dict:
+def gemm(m: int, n: int, k: int, tile: int = -1, iters: int = 20, swiglu: bool = False, rotate: int = 1) -> dict:
+    """``K.linear`` at M x N x K (BF16 in, BF16 out; with ``swiglu`` the N columns are interleaved
+    w1 | w3 pairs and the output has N / 2). With ``rotate`` > 1 each call takes the next of that
+    many weight copies, so with six copies of a large weight (more than the 256 MB Infinity Cache)
+    every call reads its weight from HBM, as the denoise step does; one copy stays cache-resident."""
     a = torch.randn(m, k, device="cuda").to(torch.bfloat16)
-    w = (0.02 * torch.randn(n, k, device="cuda")).to(torch.bfloat16)
-    out = torch.empty(m, n, device="cuda", dtype=torch.bfloat16)
+    ws = [(0.02 * torch.randn(n, k, device="cuda")).to(torch.bfloat16) for _ in range(max(rotate, 1))]
+    out = torch.empty(m, n // 2 if swiglu else n, device="cuda", dtype=torch.bfloat16)
     _lib.call("iris_gemm_force_tile", tile)
     try:
-        ms = _time(lambda i: K.linear(a, w, out=out), iters)
+        ms = _time(lambda i: K.linear(a, ws[i % len(ws)], out=out, swiglu=swiglu), iters)
     finally:
         _lib.call("iris_gemm_force_tile", -1)
     tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-    return {"kernel": "gemm_bf16", "m": m, "n": n, "k": k, "tile": tile, "us": ms * 1e3, "TFLOP/s": tflops,
-            "mfma_frac": tflops / MFMA_TFLOPS}
+    return {"kernel": "gemm_bf16_swiglu" if swiglu else "gemm_bf16", "m": m, "n": n, "k": k, "tile": tile,
+            "weight_copies": len(ws), "us": ms * 1e3, "TFLOP/s": tflops, "mfma_frac": tflops / MFMA_TFLOPS}
 
 
 def attention(b: int, h: int, hkv: int, n: int, iters: int = 20) -> dict:
@@ -182,6 +186,8 @@ def main() -> None:
     p.add_argument("n", type=int)
     p.add_argument("k", type=int)
     p.add_argument("--tile", type=int, default=-1)
+    p.add_argument("--swiglu", action="store_true")
+    p.add_argument("--rotate", type=int, default=1)
     p = sub.add_parser("attention")
     for name in ("b", "h", "hkv", "n"):
         p.add_argument(name, type=int)
@@ -195,7 +201,7 @@ def main() -> None:
     if args.cmd == "fused-ops":
         out = fused_ops()
     elif args.cmd == "gemm":
-        out = gemm(args.m, args.n, args.k, args.tile)
+        out = gemm(args.m, args.n, args.k, args.tile, swiglu=args.swiglu, rotate=args.rotate)
     elif args.cmd == "attention":
         out = attention(args.b, args.h, args.hkv, args.n)
     elif args.cmd == "encode-text":
