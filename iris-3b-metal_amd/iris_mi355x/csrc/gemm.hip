@@ -734,7 +734,8 @@ int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) 
 }
 
 // Tile shape: the candidate with the least estimated time, rounds of workgroups over the
-// 256 CUs (the last round costs as much as a full one) x tile area / relative per-CU rate.
+// device's CUs (256 on MI355X; the last round costs as much as a full one) x tile area /
+// relative per-CU rate.
 // Rates were measured on the trunk and pixel-stage shapes (sustained runs): 256x256 with eight
 // 128x64 waves 1.09, with four 128x128 waves (register-staged refills) 1.05, 192x256 0.98,
 // 256x192 0.96, 128x128 at two workgroups per CU 0.9. The SwiGLU epilogue excludes the
@@ -746,6 +747,7 @@ int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
     double rate;
   };
   const Candidate candidates[] = {{1, 1, 1.09}, {11, 1, 1.05}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
+  const int cus = device_cus();
   int best = 1;
   double best_cost = 0.0;
   for (const Candidate& c : candidates) {
@@ -754,7 +756,7 @@ int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
     if (epilogue == IRIS_EPI_SILU && t.w4) continue;
     long tiles = 0;
     for (int i = 0; i < groups; ++i) tiles += static_cast<long>((m[i] + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
-    const long slots = 256L * c.per_cu;
+    const long slots = static_cast<long>(cus) * c.per_cu;
     const double cost = static_cast<double>((tiles + slots - 1) / slots) * t.bm * t.bn * c.per_cu / c.rate;
     if (best_cost == 0.0 || cost < best_cost) best = c.tile, best_cost = cost;
   }
