@@ -2,7 +2,7 @@
 
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench fused-ops
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench gemm 4352 6400 2560 [--swiglu] [--rotate 6]
-    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench attention 1 20 5 4352
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench attention 1 20 5 4352 [--variant 4]
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench copy 1
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench encode-text 1 200
 
@@ -138,15 +138,22 @@ def gemm(m: int, n: int, k: int, tile: int = -1, iters: int = 20, swiglu: bool =
             "weight_copies": len(ws), "us": ms * 1e3, "TFLOP/s": tflops, "mfma_frac": tflops / MFMA_TFLOPS}
 
 
-def attention(b: int, h: int, hkv: int, n: int, iters: int = 20) -> dict:
+def attention(b: int, h: int, hkv: int, n: int, iters: int = 20, variant: int = -1) -> dict:
+    """``K.flash_attention`` over ``n`` tokens; ``variant`` >= 0 forces that kernel variant (an index
+    of the library's variant table, as ``iris_flash_attn_force_variant`` takes), -1 the automatic one."""
     n_pad = (n + 63) // 64 * 64
     q = torch.randn(b, h, n_pad, 128, device="cuda").to(torch.bfloat16)
     k = torch.randn(b, hkv, n_pad, 128, device="cuda").to(torch.bfloat16)
     vt = torch.randn(b, hkv, 128, n_pad, device="cuda").to(torch.bfloat16)
     out = torch.empty(b * n, h * 128, device="cuda", dtype=torch.bfloat16)
-    ms = _time(lambda i: K.flash_attention(q, k, vt, n, None, out, 0), iters)
+    _lib.call("iris_flash_attn_force_variant", variant)
+    try:
+        ms = _time(lambda i: K.flash_attention(q, k, vt, n, None, out, 0), iters)
+    finally:
+        _lib.call("iris_flash_attn_force_variant", -1)
     tflops = 4.0 * b * n * n * h * 128 / (ms * 1e-3) / 1e12
-    return {"kernel": "flash_attn", "b": b, "heads": h, "kv_heads": hkv, "n": n, "us": ms * 1e3, "TFLOP/s": tflops,
+    return {"kernel": "flash_attn", "variant": variant, "b": b, "heads": h, "kv_heads": hkv, "n": n, "us": ms * 1e3,
+            "TFLOP/s": tflops,
             "mfma_frac": tflops / MFMA_TFLOPS}
 
 
@@ -191,6 +198,7 @@ def main() -> None:
     p = sub.add_parser("attention")
     for name in ("b", "h", "hkv", "n"):
         p.add_argument(name, type=int)
+    p.add_argument("--variant", type=int, default=-1)
     p = sub.add_parser("copy")
     p.add_argument("gib", type=float, nargs="?", default=1.0)
     p = sub.add_parser("encode-text")
@@ -203,7 +211,7 @@ def main() -> None:
     elif args.cmd == "gemm":
         out = gemm(args.m, args.n, args.k, args.tile, swiglu=args.swiglu, rotate=args.rotate)
     elif args.cmd == "attention":
-        out = attention(args.b, args.h, args.hkv, args.n)
+        out = attention(args.b, args.h, args.hkv, args.n, variant=args.variant)
     elif args.cmd == "encode-text":
         out = encode_text(args.batch, args.real)
     else:
