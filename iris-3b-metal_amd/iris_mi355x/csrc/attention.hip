@@ -405,8 +405,8 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
                "flash_attn: query heads %d must be a multiple of K/V heads %d", heads, kv_heads);
   const int group = heads / kv_heads;
   IRIS_REQUIRE((group & (group - 1)) == 0, "flash_attn: heads per K/V head must be a power of two (got %d)", group);
-  IRIS_REQUIRE(n > 0 && n_pad >= n && n_pad % 64 == 0 && n_pad < (1L << 24),
-               "flash_attn: n_pad must be n rounded up to a multiple of 64");
+  IRIS_REQUIRE(n > 0 && n_pad >= n && n_pad % 64 == 0 && n_pad < (1L << 23),
+               "flash_attn: n_pad must be n rounded up to a multiple of 64, below 2^23 (32-bit byte offsets)");
   IRIS_REQUIRE(n_split >= 0 && n_split <= n, "flash_attn: n_split outside [0, n]");
   IRIS_REQUIRE(ld_out >= heads * 128L && ld_out % 4 == 0, "flash_attn: bad ld_out");
   IRIS_REQUIRE((!gate0 && !gate1) || (ld_gate >= heads * 128L && ld_gate % 4 == 0), "flash_attn: bad ld_gate");
@@ -489,8 +489,8 @@ extern "C" int iris_flash_attn_masked(const void* q, const void* k, const void* 
   const int group = heads / kv_heads;
   IRIS_REQUIRE((group & (group - 1)) == 0, "flash_attn_masked: heads per K/V head must be a power of two (got %d)",
                group);
-  IRIS_REQUIRE(n > 0 && n_pad >= n && n_pad % 64 == 0 && n_pad < (1L << 24),
-               "flash_attn_masked: n_pad must be n rounded up to a multiple of 64");
+  IRIS_REQUIRE(n > 0 && n_pad >= n && n_pad % 64 == 0 && n_pad < (1L << 23),
+               "flash_attn_masked: n_pad must be n rounded up to a multiple of 64, below 2^23 (32-bit byte offsets)");
   IRIS_REQUIRE(ld_out >= heads * 128L && ld_out % 4 == 0 && out_batch_rows >= n, "flash_attn_masked: bad output strides");
   IRIS_REQUIRE(q && k && vt && key_mask && out, "flash_attn_masked: null pointer");
   IRIS_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(vt, 16) && aligned(key_mask, 4) && aligned(out, 8),

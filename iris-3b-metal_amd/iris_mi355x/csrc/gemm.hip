@@ -798,9 +798,10 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
     IRIS_REQUIRE(!bias || !bias[i] || epilogue != IRIS_EPI_SILU_MUL, "gemm: bias is not supported with SwiGLU");
     m_total += m[i];
   }
-  IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 31), "gemm: weight too large for 32-bit offsets");
+  // byte offsets and buffer sizes are 32-bit ints (elements x 2): below 2 GiB per operand
+  IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 30), "gemm: weight above 2 GiB (32-bit byte offsets)");
   for (int i = 0; i < groups; ++i)
-    IRIS_REQUIRE(static_cast<long>(m[i]) * lda < (1L << 31), "gemm: activation too large for 32-bit offsets");
+    IRIS_REQUIRE(static_cast<long>(m[i]) * lda < (1L << 30), "gemm: activation above 2 GiB (32-bit byte offsets)");
   const int tile = pick_tile(m, groups, n, epilogue, g_forced_tile);
   const TileShape shape = kTiles[tile];
   const int bm = shape.bm;

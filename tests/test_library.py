@@ -79,3 +79,14 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
                   1 << 20, 1e-6, 1 << 20, _lib.F32, 1 << 20, None)
     with pytest.raises(ValueError, match="3 or 1 output channels"):
         _lib.call("iris_unpatchify_head", 1 << 20, 1 << 20, 1 << 20, 1 << 20, 2, 1, 32, 32, 16, None)
+    # the kernels address operands by 32-bit byte offsets: 2 GiB per operand is refused
+    k = 8192
+    with pytest.raises(ValueError, match="weight above 2 GiB"):
+        _lib.call("iris_gemm_bf16", 1 << 20, 1 << 20, None, 1 << 20, _lib.BF16, 8, (1 << 30) // k, k, k, k,
+                  (1 << 30) // k, 0, None)
+    with pytest.raises(ValueError, match="activation above 2 GiB"):
+        _lib.call("iris_gemm_bf16", 1 << 20, 1 << 20, None, 1 << 20, _lib.BF16, (1 << 30) // k, 64, k, k, k, 64, 0,
+                  None)
+    with pytest.raises(ValueError, match="below 2\\^23"):
+        _lib.call("iris_flash_attn", 1 << 20, 1 << 20, 1 << 20, 1, 4, 1, 1 << 23, 1 << 23, 0, 0.1, None, 1 << 20,
+                  512, 0, 1 << 23, None, None, 0, 0, 0, None)
