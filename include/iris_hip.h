@@ -109,17 +109,21 @@ int iris_qkv_prepare(const void* src, void* q, void* k, void* vt, const float* q
  * row (b*out_batch_rows1 + r - n_split), column h*128 + d, BF16, row stride ld_out; a null out
  * pointer skips its rows. With gate0/gate1 (rows b*gate_batch_rows{0,1} + r or r - n_split,
  * stride ld_gate) the stored value is multiplied by sigmoid(gate) (the attention gate of
- * src/iris_metal/model.py:282-283, 309). */
+ * src/iris_metal/model.py:282-283, 309). Operands are addressed with 32-bit byte offsets:
+ * n_pad < 2^23 (IRIS_E_INVALID otherwise). */
 int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int heads, int kv_heads, long n,
                     long n_pad, long n_split, float scale, void* out0, void* out1, long ld_out,
                     long out_batch_rows0, long out_batch_rows1, const void* gate0, const void* gate1, long ld_gate,
                     long gate_batch_rows0, long gate_batch_rows1, hipStream_t stream);
 
-/* Tuning hook for the benchmark sweep: force the attention variant (32 query rows per wave in
- * all; 0: 64-key tiles staged through registers, 1: 32-key tiles staged through registers,
- * 2: 64-key tiles in a 2-stage global_load_lds ring, 3: 32-key tiles in a 3-stage ring) or
- * restore the automatic choice (-1: variant 1 when four or more query heads share a K/V head,
- * else variant 2).
+/* Tuning hook for the benchmark sweep and the variant tests: force the attention variant of
+ * later iris_flash_attn calls made by the calling thread (32 query rows per wave in all;
+ * 0: 64-key tiles staged through registers, 1: 32-key tiles staged through registers,
+ * 2: 64-key tiles in a 2-stage global_load_lds ring, 3: 32-key tiles in a 3-stage ring,
+ * 4: 32-key tiles in a 3-stage ring shared by twelve waves, four query heads by three 32-row
+ * blocks) or restore the automatic choice (-1: with four or more query heads per K/V head,
+ * variant 4 when its grid of batch * kv_heads * ceil(n / 96) workgroups fills at least 80% of
+ * its rounds over the CUs, else variant 1; with fewer, variant 2). The setting is per thread.
  * No counterpart in the reference. */
 int iris_flash_attn_force_variant(int variant);
 
@@ -127,7 +131,8 @@ int iris_flash_attn_force_variant(int variant);
  * src/iris3b/nn/attention.py:117-132, src/iris3b/nn/embeddings.py:196-205): as iris_flash_attn
  * with n_split = 0 and no gate, except that query q of batch b attends key j < n only where
  * key_mask[b * n_pad + j] != 0 or j == q. key_mask: [batch, n_pad] bytes, 4-byte aligned (as
- * written by iris_text_key_mask). Output row r of batch b goes to out row b*out_batch_rows + r. */
+ * written by iris_text_key_mask). Output row r of batch b goes to out row b*out_batch_rows + r.
+ * n_pad < 2^23, as for iris_flash_attn. */
 int iris_flash_attn_masked(const void* q, const void* k, const void* vt, int batch, int heads, int kv_heads, long n,
                            long n_pad, float scale, const void* key_mask, void* out, long ld_out, long out_batch_rows,
                            hipStream_t stream);
@@ -159,18 +164,21 @@ int iris_layer_pool(const float* h, const void* branch, const float* weight, con
  * (rows 64p..64p+31 = w1 rows 32p.., rows 64p+32..64p+63 = w3 rows 32p..) and
  * C[m, j] = silu(a_j) * b_j is n/2 wide (SwiGLU, src/iris3b/nn/mlp.py:24-40).
  * IRIS_EPI_SILU: C = silu(A B^T + bias) (the Linear + SiLU of the layer-wise text adapter's
- * MLP, src/iris3b/nn/embeddings.py:131-135). */
+ * MLP, src/iris3b/nn/embeddings.py:131-135). Operands are addressed with 32-bit byte offsets:
+ * m * lda and n * ldb below 2^30 elements (2 GiB), else IRIS_E_INVALID before any launch. */
 int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n, int k,
                    long lda, long ldb, long ldc, int epilogue, hipStream_t stream);
 
-/* Tuning hook for the benchmark sweep: force the GEMM tile (an index into the tile table of
- * gemm.hip: 0-10 eight- and four-wave tiles of 256x256, 256x192, 192x256 and 128x128; 11 the
- * four-wave 128x128-per-wave kernel) or restore the automatic choice (-1). No counterpart in
- * the reference. */
+/* Tuning hook for the benchmark sweep and the tile tests: force the GEMM tile of later
+ * iris_gemm_bf16* calls made by the calling thread (an index into the tile table of gemm.hip:
+ * 0-10 eight- and four-wave tiles of 256x256, 256x192, 192x256 and 128x128; 11 the four-wave
+ * 128x128-per-wave kernel, never chosen automatically) or restore the automatic choice (-1).
+ * The setting is per thread. No counterpart in the reference. */
 int iris_gemm_force_tile(int tile);
 
 /* Up to two GEMMs of equal n, k and strides in one launch (the image and text streams of a
- * dual-stream block, src/iris_metal/model.py:273-289). */
+ * dual-stream block, src/iris_metal/model.py:273-289); each group's operands below 2 GiB, as
+ * for iris_gemm_bf16. */
 int iris_gemm_bf16_grouped(int groups, const void* const* a, const void* const* b, const float* const* bias,
                            void* const* c, const int* m, int c_dtype, int n, int k, long lda, long ldb, long ldc,
                            int epilogue, hipStream_t stream);

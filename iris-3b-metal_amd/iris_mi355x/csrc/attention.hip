@@ -390,7 +390,8 @@ struct Variant {
 constexpr Variant kVariants[] = {
     {1, 2, 64, true}, {1, 2, 32, true}, {1, 2, 64, false}, {1, 3, 32, false}, {1, 3, 32, false, 12}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
-int g_attn_variant = -1;
+// per thread: a forced variant never changes another thread's launches
+thread_local int g_attn_variant = -1;
 
 }  // namespace
 }  // namespace iris

@@ -746,7 +746,8 @@ int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
     int tile, per_cu;
     double rate;
   };
-  const Candidate candidates[] = {{1, 1, 1.09}, {11, 1, 1.05}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
+  // (tile 11 has tile 1's shape at a lower rate: forced only)
+  const Candidate candidates[] = {{1, 1, 1.09}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
   const int cus = device_cus();
   int best = 1;
   double best_cost = 0.0;
@@ -763,7 +764,8 @@ int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
   return best;
 }
 
-int g_forced_tile = -1;
+// per thread: a forced tile never changes another thread's launches
+thread_local int g_forced_tile = -1;
 
 }  // namespace
 }  // namespace iris

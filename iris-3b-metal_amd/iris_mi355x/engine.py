@@ -378,12 +378,7 @@ class HipIris:
                          ws["patches"], ws["pixels"], ws["hpix"])
         K.linear(ws["patches"], self.s_w, self.s_b, out=ws["X"])
 
-        # timestep embedding, then both shared adaLN cores with every block's bias folded in
-        K.timestep_features(t, self.t_freqs, ws["tfeat"])
-        K.gemv(self.t0_w, ws["tfeat"], self.t0_b, ws["th"], out_silu=True)
-        K.gemv(self.t2_w, ws["th"], self.t2_b, ws["temb"])
-        K.gemv(self.core_img_w, ws["temb"], self.core_img_b, ws["mods_img"], extra_bias=self.img_bias, in_silu=True)
-        K.gemv(self.core_txt_w, ws["temb"], self.core_txt_b, ws["mods_txt"], extra_bias=self.txt_bias, in_silu=True)
+        self._conditioning(ws, t)
 
         Y = ws["Y"]
         K.copy_rows(text.reshape(B * T, D), Y, B, T, 0, T, 0, T)
@@ -409,6 +404,66 @@ class HipIris:
             next_norm = self.pixel_blocks[j + 1]["norm1"] if j + 1 < len(self.pixel_blocks) else self.final_norm
             self._pixel_block(ws, pblk, B, Lp, next_norm)
         K.unpatchify_head(ws["hpix"], self.final_w, self.final_b, out, p)
+
+    def _conditioning(self, ws: dict, t: torch.Tensor) -> None:
+        """Timestep embedding, then both shared adaLN cores with every block's bias folded in."""
+        K.timestep_features(t, self.t_freqs, ws["tfeat"])
+        K.gemv(self.t0_w, ws["tfeat"], self.t0_b, ws["th"], out_silu=True)
+        K.gemv(self.t2_w, ws["th"], self.t2_b, ws["temb"])
+        K.gemv(self.core_img_w, ws["temb"], self.core_img_b, ws["mods_img"], extra_bias=self.img_bias, in_silu=True)
+        K.gemv(self.core_txt_w, ws["temb"], self.core_txt_b, ws["mods_txt"], extra_bias=self.txt_bias, in_silu=True)
+
+    @torch.no_grad()
+    def block_forward(self, index: int, x: torch.Tensor, text: torch.Tensor, t: torch.Tensor,
+                      grid: tuple[int, int]) -> tuple[torch.Tensor, torch.Tensor]:
+        """One trunk block on its own: ``x`` image tokens ``[B, L, D]`` over a ``grid`` of patches
+        (``L = grid[0] * grid[1]``), ``text`` tokens ``[B, T, D]``, model time ``t`` ``[B]``.
+        Returns the block's ``(x, text)`` as the reference block's ``forward`` does
+        (src/iris3b/models/blocks/mmdit.py:84-128, single_stream.py:69-88): FP32, the text
+        returned unchanged by a block without a text output. The modulation comes from ``t``
+        through the timestep embedder and the shared adaLN cores, as in the full forward."""
+        cfg = self.cfg
+        if not 0 <= index < cfg.depth:
+            raise ValueError(f"block index must be in [0, {cfg.depth}), got {index}")
+        B, Lp, D = x.shape
+        T = text.shape[1]
+        if grid[0] * grid[1] != Lp or text.shape[0] != B or text.shape[2] != D or D != cfg.hidden_size:
+            raise ValueError(f"x must be [B, {grid[0] * grid[1]}, {cfg.hidden_size}] and text [B, T, "
+                             f"{cfg.hidden_size}], got {tuple(x.shape)} and {tuple(text.shape)}")
+        p = cfg.patch_size
+        ws = self._workspace(_Shape(B, grid[0] * p, grid[1] * p, T))
+        dev = self.device
+        x = x.to(dev, torch.float32).contiguous()
+        text = text.to(dev, torch.float32).contiguous()
+        self._conditioning(ws, t.reshape(B).to(dev, torch.float32).contiguous())
+        N = T + Lp
+        if cfg.block_kind(index) == "mmdit":
+            ws["X"].copy_(x.reshape(B * Lp, D))
+            ws["Y"].copy_(text.reshape(B * T, D))
+        else:
+            K.copy_rows(text.reshape(B * T, D), ws["tok"], B, T, 0, T, 0, N)
+            K.copy_rows(x.reshape(B * Lp, D), ws["tok"], B, Lp, 0, Lp, T, N)
+        ws["block"] = (index, B, T, Lp, N)
+        self.run_block()
+        if cfg.block_kind(index) == "mmdit":
+            return ws["X"].view(B, Lp, D).clone(), ws["Y"].view(B, T, D).clone()
+        if not cfg.text_out(index):
+            return ws["X"].view(B, Lp, D).clone(), text
+        tok = ws["tok"].view(B, N, D)
+        return tok[:, T:].clone(), tok[:, :T].clone()
+
+    def run_block(self) -> None:
+        """Run the block of the last ``block_forward`` call again, in place on the residual it
+        left in the engine's workspace (for timing the block's kernels alone)."""
+        ws = self._ws
+        if ws is None or "block" not in ws:
+            raise RuntimeError("run_block follows a block_forward call")
+        index, B, T, Lp, N = ws["block"]
+        blk = self.blocks[index]
+        if blk["kind"] == "mmdit":
+            self._dual_block(ws, blk, B, T, Lp, N, False, None)
+        else:
+            self._single_block(ws, blk, B, T, Lp, N, not self.cfg.text_out(index), False, None)
 
     def _mods(self, ws: dict, table: str, index: int, chunk: int) -> torch.Tensor:
         D = self.cfg.hidden_size

@@ -20,30 +20,65 @@ HEAD_DIM = 128
 PIXEL_WIDTH, PIXEL_HIDDEN = 16, 64
 
 
-def _require(condition: bool, message: str) -> None:
-    if not condition:
-        raise ValueError(message)
+class _Check:
+    """The host-side argument checks of one wrapper call, run before anything is launched.
+
+    Created with the operation's name and the tensors that must live on the GPU (``None``
+    entries are skipped); calling it with a condition and a description raises
+    ``ValueError("<op>: <description>")`` when the condition is false. Methods cover the
+    recurring expectations (FP32 gains of a given width, BF16 operands, contiguity)."""
+
+    __slots__ = ("op",)
+
+    def __init__(self, op: str, *tensors: torch.Tensor | None):
+        self.op = op
+        if any(t is not None and t.device.type != "cuda" for t in tensors):
+            raise ValueError(f"{op}: the HIP kernels need GPU tensors (there is no CPU path)")
+
+    def __call__(self, ok: bool, what: str) -> "_Check":
+        if not ok:
+            raise ValueError(f"{self.op}: {what}")
+        return self
+
+    def fp32(self, **tensors: torch.Tensor) -> "_Check":
+        for name, t in tensors.items():
+            self(t.dtype == torch.float32 and t.is_contiguous(), f"{name} must be contiguous FP32 (got {t.dtype})")
+        return self
+
+    def gains(self, width: int, **gains: torch.Tensor) -> "_Check":
+        """Per-channel FP32 vectors of ``width`` entries (RMSNorm gains)."""
+        self.fp32(**gains)
+        for name, g in gains.items():
+            self(g.numel() == width, f"{name}: gain width {g.numel()} does not match the {width} channels")
+        return self
+
+    def bf16(self, **tensors: torch.Tensor) -> "_Check":
+        for name, t in tensors.items():
+            self(t.dtype == torch.bfloat16 and t.is_contiguous(), f"{name} must be contiguous BF16 (got {t.dtype})")
+        return self
 
 
-def _require_fp32(**tensors: torch.Tensor) -> None:
-    for name, tensor in tensors.items():
-        _require(tensor.dtype == torch.float32 and tensor.is_contiguous(), f"{name} must be contiguous FP32")
-
-
-def _on_gpu(*tensors: torch.Tensor) -> None:
-    for t in tensors:
-        if t is not None and t.device.type != "cuda":
-            raise ValueError("the HIP kernels need GPU tensors (there is no CPU path)")
-
-
-def _per_batch(vector: torch.Tensor, batch: int, width: int) -> tuple[torch.Tensor, int]:
-    """``[B, 1, D]`` modulation slice -> FP32 rows read in place when 16-byte aligned, and their stride."""
+def _mod_rows(vector: torch.Tensor, batch: int, width: int) -> tuple[torch.Tensor, int]:
+    """A ``[B, 1, D]`` slice of a modulation vector as FP32 rows the kernels read with 16-byte
+    loads: returned in place when its rows are unit-stride and 16-byte aligned (slices of the
+    engine's ``[B, 6D]`` modulation table are), else as a packed copy; with the row stride in
+    elements (``D`` for one row)."""
     rows = vector.reshape(batch, width)
-    if rows.dtype != torch.float32:
-        rows = rows.float()
-    if rows.stride(1) != 1 or rows.stride(0) % 4 or rows.storage_offset() % 4:
+    rows = rows if rows.dtype == torch.float32 else rows.float()
+    in_place = rows.stride(1) == 1 and rows.storage_offset() % 4 == 0 and (batch == 1 or rows.stride(0) % 4 == 0)
+    if not in_place:
         rows = rows.contiguous()
-    return rows, rows.stride(0) if batch > 1 else width
+    return rows, (rows.stride(0) if batch > 1 else width)
+
+
+def _mod_pair(shift: torch.Tensor, scale: torch.Tensor, batch: int,
+              width: int) -> tuple[torch.Tensor, torch.Tensor, int]:
+    """``_mod_rows`` of a shift and a scale that the kernel addresses with one row stride."""
+    shift, stride_a = _mod_rows(shift, batch, width)
+    scale, stride_b = _mod_rows(scale, batch, width)
+    if stride_a != stride_b:
+        shift, scale, stride_a = shift.contiguous(), scale.contiguous(), width
+    return shift, scale, stride_a
 
 
 # ---------------------------------------------------------------------------------------
@@ -65,25 +100,22 @@ def qk_norm_rope(
     (src/iris_metal/kernels.py:334-397). ``x``: contiguous ``[B, N, W]`` whose columns
     ``[col_offset, col_offset + heads*128)`` hold the heads; ``cos``/``sin``: FP32
     ``[N_out, 64]``; rows land at ``offset + token`` of ``out`` (``[B, heads, N_out, 128]``)."""
-    _require(heads > 0 and col_offset >= 0 and offset >= 0, "heads must be positive and offsets nonnegative")
+    if heads <= 0 or min(col_offset, offset) < 0:
+        raise ValueError(f"qk_norm_rope: heads must be positive and offsets nonnegative "
+                         f"(heads={heads}, col_offset={col_offset}, offset={offset})")
     batch, tokens, width = x.shape
     if out is None:
         out = x.new_empty(batch, heads, tokens, HEAD_DIM, dtype=out_dtype or x.dtype)
-    _on_gpu(x, out, weight, cos, sin)
-    _require(
-        col_offset + heads * HEAD_DIM <= width and x.is_contiguous(),
-        "qk_norm_rope needs a contiguous [B, N, W] input holding the heads",
-    )
-    _require(
-        out.shape[:2] == (batch, heads) and out.shape[3] == HEAD_DIM and out.is_contiguous(),
-        f"qk_norm_rope output must be a contiguous [{batch}, {heads}, N, {HEAD_DIM}] tensor",
-    )
-    _require(
-        cos.shape == sin.shape == (cos.shape[0], HEAD_DIM // 2) and offset + tokens <= min(cos.shape[0], out.shape[2]),
-        "qk_norm_rope rotary tables or output do not cover the written rows",
-    )
-    _require_fp32(weight=weight, cos=cos, sin=sin)
-    _require(weight.numel() == HEAD_DIM, f"qk_norm_rope gain must have {HEAD_DIM} entries")
+    check = _Check("qk_norm_rope", x, out, weight, cos, sin)
+    check(x.is_contiguous() and col_offset + heads * HEAD_DIM <= width,
+          f"the contiguous [B, N, {width}] input does not hold {heads} heads from column {col_offset}")
+    check(out.is_contiguous() and out.dim() == 4 and out.shape[:2] == (batch, heads) and out.shape[3] == HEAD_DIM,
+          f"output must be a contiguous [{batch}, {heads}, N, {HEAD_DIM}] tensor")
+    rows_needed = offset + tokens
+    check(cos.shape == sin.shape and cos.dim() == 2 and cos.shape[1] == HEAD_DIM // 2
+          and rows_needed <= cos.shape[0] and rows_needed <= out.shape[2],
+          f"rotary tables or output do not cover the written rows (up to {rows_needed})")
+    check.fp32(cos=cos, sin=sin).gains(HEAD_DIM, weight=weight)
     L.call(
         "iris_qk_norm_rope", L.ptr(x), L.dtype_code(x.dtype), L.ptr(out), L.dtype_code(out.dtype), L.ptr(weight),
         L.ptr(cos), L.ptr(sin), cos.shape[0], batch, tokens, out.shape[2], heads, offset, width, col_offset,
@@ -104,24 +136,27 @@ def rms_norm_modulate(
     """``(rms_norm(x) * weight * (1 + scale) + shift).to(out_dtype)`` for ``x``: ``[B, N, D]`` and
     per-sample ``shift``/``scale``: ``[B, 1, D]`` (src/iris_metal/kernels.py:413-452)."""
     batch, tokens, width = x.shape
-    _on_gpu(x, weight, shift, scale)
-    _require(width % 128 == 0 and x.is_contiguous(), "rms_norm_modulate needs a contiguous input, width % 128 == 0")
-    _require_fp32(weight=weight)
-    _require(weight.numel() == width, "rms_norm_modulate gain width mismatch")
+    check = _Check("rms_norm_modulate", x, weight, shift, scale, out)
+    check(x.is_contiguous() and width % 128 == 0, f"needs a contiguous input whose width is a multiple of 128 "
+                                                  f"(got {width})")
+    check.gains(width, weight=weight)
     if out is None:
         out = torch.empty(x.shape, device=x.device, dtype=out_dtype)
-    _require(out.shape == x.shape and out.is_contiguous() and out.dtype == out_dtype, "rms_norm_modulate: bad out")
-    shift, shift_stride = _per_batch(shift, batch, width)
-    scale, scale_stride = _per_batch(scale, batch, width)
-    if shift_stride != scale_stride:  # the kernel takes one stride
-        shift, scale = shift.contiguous(), scale.contiguous()
-        shift_stride = width
+    check(out.is_contiguous() and out.shape == x.shape and out.dtype == out_dtype,
+          f"out must be a contiguous {out_dtype} tensor of the input's shape")
+    shift, scale, stride = _mod_pair(shift, scale, batch, width)
     L.call(
         "iris_rms_norm_modulate", L.ptr(x), L.dtype_code(x.dtype), L.ptr(out), L.dtype_code(out_dtype),
-        L.ptr(weight), L.ptr(shift), L.ptr(scale), batch * tokens, tokens, width, shift_stride, float(eps),
+        L.ptr(weight), L.ptr(shift), L.ptr(scale), batch * tokens, tokens, width, stride, float(eps),
         L.stream(),
     )
     return out
+
+
+def _residual_checks(check: _Check, residual: torch.Tensor, branch: torch.Tensor, width: int) -> None:
+    check(width % 128 == 0 and branch.shape == residual.shape and branch.is_contiguous(),
+          "the branch must be contiguous and shaped like the residual, of a width that is a multiple of 128")
+    check.fp32(residual=residual)
 
 
 def gated_residual_rms_norm_(
@@ -130,12 +165,10 @@ def gated_residual_rms_norm_(
     """``residual += gate * rms_norm(branch) * weight`` in place; ``residual``: FP32 ``[B, N, D]``
     (src/iris_metal/kernels.py:455-480)."""
     batch, tokens, width = residual.shape
-    _on_gpu(residual, branch, weight, gate)
-    _require(width % 128 == 0 and branch.shape == residual.shape, "gated_residual_rms_norm_ shape mismatch")
-    _require(branch.is_contiguous(), "gated_residual_rms_norm_ needs a contiguous branch")
-    _require_fp32(residual=residual, weight=weight)
-    _require(weight.numel() == width, "gated_residual_rms_norm_ gain width mismatch")
-    gate, gate_stride = _per_batch(gate, batch, width)
+    check = _Check("gated_residual_rms_norm_", residual, branch, weight, gate)
+    _residual_checks(check, residual, branch, width)
+    check.gains(width, weight=weight)
+    gate, gate_stride = _mod_rows(gate, batch, width)
     L.call(
         "iris_gated_residual_rms_norm", L.ptr(residual), L.ptr(branch), L.dtype_code(branch.dtype), L.ptr(weight),
         L.ptr(gate), batch * tokens, tokens, width, gate_stride, float(eps), L.stream(),
@@ -150,22 +183,17 @@ def gated_residual_norm_modulate_(
     """``gated_residual_rms_norm_`` then ``rms_norm_modulate`` of the updated residual into ``out``,
     in one pass over the row (the residual is read and written once)."""
     batch, tokens, width = residual.shape
-    _on_gpu(residual, branch, weight, gate, next_weight, next_shift, next_scale, out)
-    _require(width % 128 == 0 and branch.shape == residual.shape, "gated_residual_rms_norm_ shape mismatch")
-    _require(branch.is_contiguous() and out.is_contiguous() and out.shape == residual.shape,
-             "gated_residual_norm_modulate_ needs contiguous branch and output")
-    _require_fp32(residual=residual, weight=weight, next_weight=next_weight)
-    _require(weight.numel() == next_weight.numel() == width, "gated_residual_norm_modulate_ gain width mismatch")
-    gate, gate_stride = _per_batch(gate, batch, width)
-    shift, shift_stride = _per_batch(next_shift, batch, width)
-    scale, scale_stride = _per_batch(next_scale, batch, width)
-    if shift_stride != scale_stride:
-        shift, scale = shift.contiguous(), scale.contiguous()
-        shift_stride = width
+    check = _Check("gated_residual_norm_modulate_", residual, branch, weight, gate, next_weight, next_shift,
+                   next_scale, out)
+    _residual_checks(check, residual, branch, width)
+    check(out.is_contiguous() and out.shape == residual.shape, "out must be contiguous and shaped like the residual")
+    check.gains(width, weight=weight, next_weight=next_weight)
+    gate, gate_stride = _mod_rows(gate, batch, width)
+    shift, scale, stride = _mod_pair(next_shift, next_scale, batch, width)
     L.call(
         "iris_gated_residual_norm_modulate", L.ptr(residual), L.ptr(branch), L.dtype_code(branch.dtype),
         L.ptr(weight), L.ptr(gate), batch * tokens, tokens, width, gate_stride, float(eps), L.ptr(next_weight),
-        L.ptr(shift), L.ptr(scale), shift_stride, L.ptr(out), L.dtype_code(out.dtype), L.stream(),
+        L.ptr(shift), L.ptr(scale), stride, L.ptr(out), L.dtype_code(out.dtype), L.stream(),
     )
     return out
 
@@ -175,44 +203,36 @@ def gated_residual_grouped_(residuals, branches, weights, gates, eps: float, nex
     """``gated_residual_rms_norm_`` (``outs`` None) or ``gated_residual_norm_modulate_`` of two
     streams (the image and text rows of a dual-stream block) in one launch, each on its own
     tensors; same results as the two calls."""
-    _require(len(residuals) == len(branches) == len(weights) == len(gates) == 2, "gated_residual_grouped_ takes two")
+    if not len(residuals) == len(branches) == len(weights) == len(gates) == 2:
+        raise ValueError("gated_residual_grouped_ takes two streams")
     nxt = outs is not None
     width = residuals[0].shape[-1]
-    keep, rows, per_batch, strides, nstrides, shifts, scales = [], [], [], [], [], [], []
+    groups = []  # per stream: (gate rows, rows, rows per batch, gate stride, shift, scale, stride)
     for i in range(2):
         residual, branch = residuals[i], branches[i]
         batch, tokens, w = residual.shape
-        _on_gpu(residual, branch, weights[i], gates[i])
-        _require(w == width and w % 128 == 0 and branch.shape == residual.shape and branch.is_contiguous(),
-                 "gated_residual_grouped_ shape mismatch")
-        _require(branch.dtype == branches[0].dtype, "gated_residual_grouped_: branch dtypes differ")
-        _require_fp32(residual=residual, weight=weights[i])
-        _require(weights[i].numel() == width, "gated_residual_grouped_ gain width mismatch")
-        gate, gate_stride = _per_batch(gates[i], batch, width)
-        keep.append(gate)
-        rows.append(batch * tokens)
-        per_batch.append(tokens)
-        strides.append(gate_stride)
+        check = _Check(f"gated_residual_grouped_ (stream {i})", residual, branch, weights[i], gates[i],
+                       *((next_weights[i], next_shifts[i], next_scales[i], outs[i]) if nxt else ()))
+        check(w == width, "the two streams differ in width")
+        _residual_checks(check, residual, branch, width)
+        check(branch.dtype == branches[0].dtype, "the two branches differ in dtype")
+        check.gains(width, weight=weights[i])
+        gate, gate_stride = _mod_rows(gates[i], batch, width)
+        entry = [gate, batch * tokens, tokens, gate_stride, None, None, 0]
         if nxt:
-            _on_gpu(next_weights[i], next_shifts[i], next_scales[i], outs[i])
-            _require(outs[i].is_contiguous() and outs[i].shape == residual.shape and outs[i].dtype == outs[0].dtype,
-                     "gated_residual_grouped_: bad output")
-            _require_fp32(next_weight=next_weights[i])
-            shift, shift_stride = _per_batch(next_shifts[i], batch, width)
-            scale, scale_stride = _per_batch(next_scales[i], batch, width)
-            if shift_stride != scale_stride:
-                shift, scale = shift.contiguous(), scale.contiguous()
-                shift_stride = width
-            shifts.append(shift)
-            scales.append(scale)
-            nstrides.append(shift_stride)
+            check(outs[i].is_contiguous() and outs[i].shape == residual.shape and outs[i].dtype == outs[0].dtype,
+                  "outputs must be contiguous, shaped like their residual, of one dtype")
+            check.gains(width, next_weight=next_weights[i])
+            entry[4:] = _mod_pair(next_shifts[i], next_scales[i], batch, width)
+        groups.append(entry)
     P = L.pointer_array
     L.call(
         "iris_gated_residual_grouped", 2, P([L.ptr(r) for r in residuals]), P([L.ptr(b) for b in branches]),
-        L.dtype_code(branches[0].dtype), P([L.ptr(w) for w in weights]), P([L.ptr(g) for g in keep]),
-        L.long_array(rows), L.long_array(per_batch), width, L.long_array(strides), float(eps),
-        P([L.ptr(w) for w in next_weights]) if nxt else None, P([L.ptr(x) for x in shifts]) if nxt else None,
-        P([L.ptr(x) for x in scales]) if nxt else None, L.long_array(nstrides) if nxt else None,
+        L.dtype_code(branches[0].dtype), P([L.ptr(w) for w in weights]), P([L.ptr(g[0]) for g in groups]),
+        L.long_array([g[1] for g in groups]), L.long_array([g[2] for g in groups]), width,
+        L.long_array([g[3] for g in groups]), float(eps),
+        P([L.ptr(w) for w in next_weights]) if nxt else None, P([L.ptr(g[4]) for g in groups]) if nxt else None,
+        P([L.ptr(g[5]) for g in groups]) if nxt else None, L.long_array([g[6] for g in groups]) if nxt else None,
         P([L.ptr(o) for o in outs]) if nxt else None, L.dtype_code(outs[0].dtype) if nxt else L.BF16, L.stream(),
     )
 
@@ -220,10 +240,9 @@ def gated_residual_grouped_(residuals, branches, weights, gates, eps: float, nex
 def pixel_rms_norm(pixels: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """``rms_norm(pixels) * weight`` over the 16 channels of each pixel, stored BF16
     (src/iris_metal/kernels.py:486-498)."""
-    _on_gpu(pixels, weight)
-    _require(pixels.shape[-1] == PIXEL_WIDTH and pixels.is_contiguous(), "pixel_rms_norm needs 16-wide pixels")
-    _require_fp32(weight=weight)
-    _require(weight.numel() == PIXEL_WIDTH, "pixel_rms_norm gain width mismatch")
+    check = _Check("pixel_rms_norm", pixels, weight)
+    check(pixels.is_contiguous() and pixels.shape[-1] == PIXEL_WIDTH, "needs contiguous 16-channel pixels")
+    check.gains(PIXEL_WIDTH, weight=weight)
     out = torch.empty(pixels.shape, device=pixels.device, dtype=torch.bfloat16)
     n_pixels = pixels.numel() // PIXEL_WIDTH
     L.call("iris_pixel_rms_norm", L.ptr(pixels), L.dtype_code(pixels.dtype), L.ptr(out), L.ptr(weight), n_pixels,
@@ -251,28 +270,18 @@ def pixel_mlp_(
     (src/iris_metal/kernels.py:527-584). ``pixels``: FP32 or BF16 ``[..., 16]`` (updated in
     place); ``branch``: BF16 ``[..., 16]``; ``mods``: BF16 ``[..., 64]`` (scale1, shift1,
     scale2, shift2); ``fc1``/``fc2``: ``nn.Linear`` (or ``(weight, bias)``) of 16 -> 64 -> 16."""
-    _on_gpu(pixels, branch, mods, norm_weight, next_norm_weight)
+    check = _Check("pixel_mlp_", pixels, branch, mods, norm_weight, next_norm_weight)
     w1, b1 = _linear_params(fc1)
     w2, b2 = _linear_params(fc2)
-    _require(
-        pixels.shape[-1] == PIXEL_WIDTH
-        and branch.shape == pixels.shape
-        and mods.shape == (*pixels.shape[:-1], 4 * PIXEL_WIDTH)
-        and w1.shape == (PIXEL_HIDDEN, PIXEL_WIDTH)
-        and w2.shape == (PIXEL_WIDTH, PIXEL_HIDDEN)
-        and b1.shape == (PIXEL_HIDDEN,)
-        and b2.shape == (PIXEL_WIDTH,),
-        "pixel_mlp_ needs the released pixel-stage widths",
-    )
-    _require(
-        all(t.is_contiguous() for t in (pixels, branch, mods))
-        and branch.dtype == torch.bfloat16
-        and mods.dtype == torch.bfloat16
-        and pixels.dtype in (torch.float32, torch.bfloat16),
-        "pixel_mlp_ needs contiguous BF16 branch/mods and FP32 or BF16 pixels",
-    )
-    _require_fp32(norm_weight=norm_weight, next_norm_weight=next_norm_weight)
-    _require(norm_weight.numel() == next_norm_weight.numel() == PIXEL_WIDTH, "pixel_mlp_ gain width mismatch")
+    widths = (pixels.shape[-1], tuple(w1.shape), tuple(w2.shape), tuple(b1.shape), tuple(b2.shape))
+    released = (PIXEL_WIDTH, (PIXEL_HIDDEN, PIXEL_WIDTH), (PIXEL_WIDTH, PIXEL_HIDDEN), (PIXEL_HIDDEN,), (PIXEL_WIDTH,))
+    check(widths == released and branch.shape == pixels.shape
+          and mods.shape == (*pixels.shape[:-1], 4 * PIXEL_WIDTH),
+          "needs the released pixel-stage widths (16 channels, a 64-wide MLP, 64 modulation values per pixel)")
+    check(pixels.dtype in (torch.float32, torch.bfloat16) and pixels.is_contiguous(),
+          "pixels must be contiguous FP32 or BF16")
+    check.bf16(branch=branch, mods=mods)
+    check.gains(PIXEL_WIDTH, norm_weight=norm_weight, next_norm_weight=next_norm_weight)
     if next_input is None:
         next_input = torch.empty(pixels.shape, device=pixels.device, dtype=torch.bfloat16)
     n_pixels = pixels.numel() // PIXEL_WIDTH
@@ -303,10 +312,10 @@ def v_heads_t(x: torch.Tensor, heads: int, out: torch.Tensor, col_offset: int = 
     (``[B, heads, 128, N_pad]``) transposed, token ``offset + t`` at position
     ``vt_positions(N_pad)[offset + t]`` (the layout ``flash_attention`` reads)."""
     batch, tokens, width = x.shape
-    _on_gpu(x, out)
-    _require(x.dtype == torch.bfloat16 and out.dtype == torch.bfloat16, "v_heads_t works on BF16")
-    _require(x.is_contiguous() and out.is_contiguous(), "v_heads_t needs contiguous tensors")
-    _require(out.shape[:3] == (batch, heads, HEAD_DIM), f"v_heads_t output must be [{batch}, {heads}, 128, N]")
+    check = _Check("v_heads_t", x, out)
+    check(x.dtype == torch.bfloat16 and out.dtype == torch.bfloat16, "works on BF16")
+    check(x.is_contiguous() and out.is_contiguous(), "needs contiguous tensors")
+    check(out.shape[:3] == (batch, heads, HEAD_DIM), f"output must be [{batch}, {heads}, 128, N]")
     L.call("iris_v_heads_t", L.ptr(x), L.ptr(out), batch, tokens, out.shape[3], heads, offset, width, col_offset,
            L.stream())
     return out
@@ -334,16 +343,16 @@ def qkv_prepare(
     ``[B, heads, N_out, 128]``, ``k``: ``[B, kv_heads, N_out, 128]``, ``vt``:
     ``[B, kv_heads, 128, N_pad]``, all BF16, rows / positions from ``offset``."""
     batch, tokens, width = x.shape
-    _on_gpu(x, q, k, vt, q_weight, k_weight, cos, sin)
-    _require(all(t.dtype == torch.bfloat16 for t in (x, q, k, vt)), "qkv_prepare works on BF16")
-    _require(x.is_contiguous() and q.is_contiguous() and k.is_contiguous() and vt.is_contiguous(),
-             "qkv_prepare needs contiguous tensors")
-    _require(q.shape == (batch, heads, q.shape[2], HEAD_DIM) and k.shape == (batch, kv_heads, q.shape[2], HEAD_DIM),
-             "qkv_prepare: q / k must be [B, heads, N, 128] buffers of equal length")
-    _require(vt.shape[:3] == (batch, kv_heads, HEAD_DIM), f"qkv_prepare: vt must be [{batch}, {kv_heads}, 128, N]")
-    _require(cos.shape == sin.shape == (cos.shape[0], HEAD_DIM // 2), "qkv_prepare: rotary tables must be [N, 64]")
-    _require_fp32(q_weight=q_weight, k_weight=k_weight, cos=cos, sin=sin)
-    _require(q_weight.numel() == HEAD_DIM and k_weight.numel() == HEAD_DIM, "qkv_prepare: gains have 128 entries")
+    check = _Check("qkv_prepare", x, q, k, vt, q_weight, k_weight, cos, sin)
+    check(all(t.dtype == torch.bfloat16 for t in (x, q, k, vt)), "works on BF16")
+    check(x.is_contiguous() and q.is_contiguous() and k.is_contiguous() and vt.is_contiguous(),
+          "needs contiguous tensors")
+    check(q.shape == (batch, heads, q.shape[2], HEAD_DIM) and k.shape == (batch, kv_heads, q.shape[2], HEAD_DIM),
+          "q / k must be [B, heads, N, 128] buffers of equal length")
+    check(vt.shape[:3] == (batch, kv_heads, HEAD_DIM), f"vt must be [{batch}, {kv_heads}, 128, N]")
+    check(cos.shape == sin.shape == (cos.shape[0], HEAD_DIM // 2), "rotary tables must be [N, 64]")
+    check.fp32(q_weight=q_weight, k_weight=k_weight, cos=cos, sin=sin)
+    check(q_weight.numel() == HEAD_DIM and k_weight.numel() == HEAD_DIM, "gains have 128 entries")
     L.call(
         "iris_qkv_prepare", L.ptr(x), L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(q_weight), L.ptr(k_weight), L.ptr(cos),
         L.ptr(sin), cos.shape[0], batch, tokens, q.shape[2], vt.shape[3], heads, kv_heads, offset, width, q_col,
@@ -366,22 +375,22 @@ def linear(
     ``[N]``. With ``swiglu`` the weight is a ``pack_swiglu`` pair and the result is
     ``silu(x w1^T) * (x w3^T)``, N/2 wide; with ``silu`` the result is ``silu(x w^T + bias)``.
     K must be a multiple of 64."""
-    _require(not (swiglu and silu), "linear: choose one epilogue")
-    _on_gpu(x, weight, bias, out)
-    _require(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, "linear takes BF16 operands")
-    _require(x.stride(-1) == 1 and weight.is_contiguous(), "linear needs row-contiguous operands")
+    _Check("linear")(not (swiglu and silu), "choose one epilogue")
+    check = _Check("linear", x, weight, bias, out)
+    check(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, "takes BF16 operands")
+    check(x.stride(-1) == 1 and weight.is_contiguous(), "needs row-contiguous operands")
     k = x.shape[-1]
     n = weight.shape[0]
-    _require(weight.shape[1] == k, f"linear: weight {tuple(weight.shape)} does not match input width {k}")
+    check(weight.shape[1] == k, f"weight {tuple(weight.shape)} does not match input width {k}")
     x2 = x.reshape(-1, k)
     m = x2.shape[0]
     n_out = n // 2 if swiglu else n
     if out is None:
         out = torch.empty(*x.shape[:-1], n_out, device=x.device, dtype=out_dtype)
-    _require(out.shape[-1] == n_out and out.stride(-1) == 1, "linear: bad output")
+    check(out.shape[-1] == n_out and out.stride(-1) == 1, "bad output")
     if bias is not None:
-        _require_fp32(bias=bias)
-        _require(bias.numel() == n, "linear: bias width mismatch")
+        check.fp32(bias=bias)
+        check(bias.numel() == n, "bias width mismatch")
     out2 = out.reshape(-1, n_out)
     L.call(
         "iris_gemm_bf16", L.ptr(x2), L.ptr(weight), L.ptr(bias), L.ptr(out2), L.dtype_code(out.dtype), m, n, k,
@@ -393,17 +402,17 @@ def linear(
 
 def linear_grouped(xs, weights, biases, outs, swiglu: bool = False) -> None:
     """Two ``linear`` calls of equal weight shape (one per stream of a dual block) in one launch."""
-    _require(len(xs) == len(weights) == len(outs) == 2, "linear_grouped takes two problems")
+    _Check("linear_grouped")(len(xs) == len(weights) == len(outs) == 2, "takes two problems")
     k = xs[0].shape[-1]
     n = weights[0].shape[0]
     for x, w, o in zip(xs, weights, outs):
-        _on_gpu(x, w, o)
-        _require(w.shape == (n, k) and x.shape[-1] == k and x.stride(-1) == 1, "linear_grouped: shape mismatch")
-        _require(x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16, "linear_grouped takes BF16 operands")
+        check = _Check("linear_grouped", x, w, o)
+        check(w.shape == (n, k) and x.shape[-1] == k and x.stride(-1) == 1, "shape mismatch")
+        check(x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16, "takes BF16 operands")
     x2 = [x.reshape(-1, k) for x in xs]
     o2 = [o.reshape(-1, o.shape[-1]) for o in outs]
-    _require(x2[0].stride(0) == x2[1].stride(0) and o2[0].stride(0) == o2[1].stride(0), "linear_grouped: strides differ")
-    _require(outs[0].dtype == outs[1].dtype, "linear_grouped: output dtypes differ")
+    check(x2[0].stride(0) == x2[1].stride(0) and o2[0].stride(0) == o2[1].stride(0), "strides differ")
+    check(outs[0].dtype == outs[1].dtype, "output dtypes differ")
     bias_ptrs = None if biases is None else L.pointer_array([L.ptr(b) for b in biases])
     L.call(
         "iris_gemm_bf16_grouped", 2, L.pointer_array([L.ptr(x) for x in x2]),
@@ -417,7 +426,7 @@ def pack_swiglu(w1: torch.Tensor, w3: torch.Tensor, hidden_pad: int) -> torch.Te
     """Interleave SwiGLU ``w1``/``w3`` (``[H, D]``) in 32-row groups, zero-padded to ``hidden_pad``
     rows each: rows ``64p..64p+31`` are ``w1[32p:32p+32]``, rows ``64p+32..`` are ``w3[32p:..]``."""
     hidden, dim = w1.shape
-    _require(w3.shape == w1.shape and hidden_pad % 32 == 0 and hidden_pad >= hidden, "pack_swiglu: bad shapes")
+    _Check("pack_swiglu")(w3.shape == w1.shape and hidden_pad % 32 == 0 and hidden_pad >= hidden, "bad shapes")
     pad = torch.zeros(2, hidden_pad, dim, dtype=w1.dtype, device=w1.device)
     pad[0, :hidden] = w1
     pad[1, :hidden] = w3
@@ -446,18 +455,18 @@ def flash_attention(
     with zero columns from ``n`` on, all BF16."""
     batch, heads, n_pad, hd = q.shape
     kv_heads = k.shape[1]
-    _on_gpu(q, k, vt, out0, out1, gate0, gate1)
-    _require(hd == HEAD_DIM and k.shape == (batch, kv_heads, n_pad, HEAD_DIM), "flash_attention: bad q/k shapes")
-    _require(vt.shape == (batch, kv_heads, HEAD_DIM, n_pad), "flash_attention: bad vt shape")
-    _require(all(t.dtype == torch.bfloat16 and t.is_contiguous() for t in (q, k, vt)), "flash_attention: BF16 inputs")
+    check = _Check("flash_attention", q, k, vt, out0, out1, gate0, gate1)
+    check(hd == HEAD_DIM and k.shape == (batch, kv_heads, n_pad, HEAD_DIM), "bad q/k shapes")
+    check(vt.shape == (batch, kv_heads, HEAD_DIM, n_pad), "bad vt shape")
+    check(all(t.dtype == torch.bfloat16 and t.is_contiguous() for t in (q, k, vt)), "BF16 inputs")
     ref = out1 if out1 is not None else out0
-    _require(ref is not None, "flash_attention: no output")
+    check(ref is not None, "no output")
     for t in (out0, out1, gate0, gate1):
         if t is not None:
-            _require(t.dtype == torch.bfloat16 and t.stride(-1) == 1, "flash_attention: BF16 row-major outputs/gates")
+            check(t.dtype == torch.bfloat16 and t.stride(-1) == 1, "BF16 row-major outputs/gates")
     ld_out = ref.stride(-2)
     if out0 is not None and out1 is not None:
-        _require(out0.stride(-2) == ld_out, "flash_attention: output strides differ")
+        check(out0.stride(-2) == ld_out, "output strides differ")
     gref = gate1 if gate1 is not None else gate0
     ld_gate = gref.stride(-2) if gref is not None else 0
     ob = out_batch_rows or (n_split, n - n_split)
@@ -477,21 +486,21 @@ def flash_attention_masked(q, k, vt, n: int, key_mask: torch.Tensor, out: torch.
     or ``[B*n, heads*128]`` with unit column stride."""
     batch, heads, n_pad, hd = q.shape
     kv_heads = k.shape[1]
-    _on_gpu(q, k, vt, key_mask, out)
-    _require(hd == HEAD_DIM and k.shape == (batch, kv_heads, n_pad, HEAD_DIM), "flash_attention_masked: bad q/k shapes")
-    _require(vt.shape == (batch, kv_heads, HEAD_DIM, n_pad), "flash_attention_masked: bad vt shape")
-    _require(all(t.dtype == torch.bfloat16 and t.is_contiguous() for t in (q, k, vt)),
-             "flash_attention_masked: BF16 inputs")
-    _require(key_mask.dtype == torch.uint8 and key_mask.shape == (batch, n_pad) and key_mask.is_contiguous(),
-             f"flash_attention_masked: key_mask must be uint8 [{batch}, {n_pad}]")
-    _require(out.dtype == torch.bfloat16 and out.stride(-1) == 1 and out.shape[-1] == heads * HEAD_DIM,
-             "flash_attention_masked: BF16 row-major output")
+    check = _Check("flash_attention_masked", q, k, vt, key_mask, out)
+    check(hd == HEAD_DIM and k.shape == (batch, kv_heads, n_pad, HEAD_DIM), "bad q/k shapes")
+    check(vt.shape == (batch, kv_heads, HEAD_DIM, n_pad), "bad vt shape")
+    check(all(t.dtype == torch.bfloat16 and t.is_contiguous() for t in (q, k, vt)),
+          "BF16 inputs")
+    check(key_mask.dtype == torch.uint8 and key_mask.shape == (batch, n_pad) and key_mask.is_contiguous(),
+          f"key_mask must be uint8 [{batch}, {n_pad}]")
+    check(out.dtype == torch.bfloat16 and out.stride(-1) == 1 and out.shape[-1] == heads * HEAD_DIM,
+          "BF16 row-major output")
     if out.dim() == 3:
-        _require(out.shape[0] == batch and out.shape[1] >= n, "flash_attention_masked: output too small")
+        check(out.shape[0] == batch and out.shape[1] >= n, "output too small")
         batch_rows = out.stride(0) // out.stride(1)
-        _require(out.stride(0) == batch_rows * out.stride(1), "flash_attention_masked: output batch stride")
+        check(out.stride(0) == batch_rows * out.stride(1), "output batch stride")
     else:
-        _require(out.shape[0] >= batch * n, "flash_attention_masked: output too small")
+        check(out.shape[0] >= batch * n, "output too small")
         batch_rows = n
     scale = HEAD_DIM ** -0.5 if scale is None else scale
     L.call("iris_flash_attn_masked", L.ptr(q), L.ptr(k), L.ptr(vt), batch, heads, kv_heads, n, n_pad, float(scale),
@@ -504,11 +513,11 @@ _MASK_KINDS = {torch.bool: 0, torch.uint8: 0, torch.int8: 0, torch.int32: 1, tor
 
 def text_key_mask(mask: torch.Tensor, n: int, out: torch.Tensor) -> torch.Tensor:
     """``mask[:, :n].bool()`` as the zero-padded uint8 ``[B, N_pad]`` key mask of ``flash_attention_masked``."""
-    _on_gpu(mask, out)
-    _require(mask.dtype in _MASK_KINDS, f"text mask dtype {mask.dtype} not supported (bool, uint8, int32, int64, float32)")
-    _require(mask.dim() == 2 and mask.stride(1) == 1 and mask.shape[1] >= n, "text mask must be [B, >= n] row-major")
-    _require(out.dtype == torch.uint8 and out.dim() == 2 and out.shape[0] == mask.shape[0] and out.is_contiguous(),
-             "text_key_mask: out must be uint8 [B, N_pad]")
+    check = _Check("text_key_mask", mask, out)
+    check(mask.dtype in _MASK_KINDS, f"text mask dtype {mask.dtype} not supported (bool, uint8, int32, int64, float32)")
+    check(mask.dim() == 2 and mask.stride(1) == 1 and mask.shape[1] >= n, "text mask must be [B, >= n] row-major")
+    check(out.dtype == torch.uint8 and out.dim() == 2 and out.shape[0] == mask.shape[0] and out.is_contiguous(),
+          "out must be uint8 [B, N_pad]")
     L.call("iris_text_key_mask", L.ptr(mask), _MASK_KINDS[mask.dtype], mask.stride(0), mask.shape[0], n, out.shape[1],
            L.ptr(out), L.stream())
     return out
@@ -518,12 +527,12 @@ def layer_attention(qkv: torch.Tensor, out: torch.Tensor, seq_len: int, heads: i
     """Attention of each text token over its ``seq_len`` encoder-layer states (no mask, no QK norm):
     ``qkv`` BF16 ``[S*seq_len, 3*heads*d]`` -> ``out`` BF16 ``[S*seq_len, heads*d]``
     (src/iris3b/nn/embeddings.py:139-141, src/iris3b/nn/attention.py:117-132)."""
-    _on_gpu(qkv, out)
+    check = _Check("layer_attention", qkv, out)
     rows, width3 = qkv.shape
-    _require(qkv.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and qkv.is_contiguous() and out.is_contiguous(),
-             "layer_attention works on contiguous BF16")
-    _require(width3 % (3 * heads) == 0 and rows % seq_len == 0 and out.shape == (rows, width3 // 3),
-             "layer_attention: bad shapes")
+    check(qkv.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and qkv.is_contiguous() and out.is_contiguous(),
+          "works on contiguous BF16")
+    check(width3 % (3 * heads) == 0 and rows % seq_len == 0 and out.shape == (rows, width3 // 3),
+          "bad shapes")
     d = width3 // (3 * heads)
     scale = d ** -0.5 if scale is None else scale
     L.call("iris_layer_attention", L.ptr(qkv), L.ptr(out), rows // seq_len, seq_len, heads, d, float(scale), L.stream())
@@ -534,18 +543,18 @@ def layer_pool(h: torch.Tensor, branch: torch.Tensor | None, weight: torch.Tenso
                layers: int, out: torch.Tensor) -> torch.Tensor:
     """``layer_pool((h + branch).transpose(1, 2)).squeeze(-1)`` over ``[R, layers, W]`` states
     (src/iris3b/nn/embeddings.py:262); ``h`` FP32, ``branch`` BF16 or None, ``out`` ``[R, W]``."""
-    _on_gpu(h, branch, weight, bias, out)
-    _require_fp32(h=h, weight=weight)
+    check = _Check("layer_pool", h, branch, weight, bias, out)
+    check.fp32(h=h, weight=weight)
     width = h.shape[-1]
     rows = h.numel() // (layers * width)
-    _require(h.is_contiguous() and h.numel() == rows * layers * width, "layer_pool: bad states")
+    check(h.is_contiguous() and h.numel() == rows * layers * width, "bad states")
     if branch is not None:
-        _require(branch.dtype == torch.bfloat16 and branch.is_contiguous() and branch.numel() == h.numel(),
-                 "layer_pool: branch must be BF16 like h")
+        check(branch.dtype == torch.bfloat16 and branch.is_contiguous() and branch.numel() == h.numel(),
+              "branch must be BF16 like h")
     if bias is not None:
-        _require_fp32(bias=bias)
-    _require(weight.numel() == layers and (bias is None or bias.numel() == 1), "layer_pool: weight is [1, layers]")
-    _require(out.is_contiguous() and out.numel() == rows * width, "layer_pool: bad out")
+        check.fp32(bias=bias)
+    check(weight.numel() == layers and (bias is None or bias.numel() == 1), "weight is [1, layers]")
+    check(out.is_contiguous() and out.numel() == rows * width, "bad out")
     L.call("iris_layer_pool", L.ptr(h), L.ptr(branch), L.ptr(weight), L.ptr(bias), rows, layers, width, L.ptr(out),
            L.dtype_code(out.dtype), L.stream())
     return out
@@ -556,20 +565,20 @@ def residual_rms_norm(residual: torch.Tensor, branch: torch.Tensor | None, weigh
     """``residual += branch`` (in place, FP32), then ``out = rmsnorm(residual) * weight (+ add_rows)``
     (the pre-norm residual of src/iris3b/nn/embeddings.py:105-107, 139-141; ``add_rows``
     ``[P, W]`` is added to row ``r`` as ``add_rows[r % P]``)."""
-    _on_gpu(residual, branch, weight, out, add_rows)
-    _require_fp32(residual=residual, weight=weight)
+    check = _Check("residual_rms_norm", residual, branch, weight, out, add_rows)
+    check.fp32(residual=residual, weight=weight)
     width = residual.shape[-1]
     rows = residual.numel() // width
-    _require(residual.is_contiguous() and out.is_contiguous() and out.numel() == residual.numel(),
-             "residual_rms_norm: contiguous residual and out of one shape")
+    check(residual.is_contiguous() and out.is_contiguous() and out.numel() == residual.numel(),
+          "contiguous residual and out of one shape")
     if branch is not None:
-        _require(branch.is_contiguous() and branch.numel() == residual.numel(), "residual_rms_norm: bad branch")
+        check(branch.is_contiguous() and branch.numel() == residual.numel(), "bad branch")
     period = 0
     if add_rows is not None:
-        _require_fp32(add_rows=add_rows)
-        _require(add_rows.is_contiguous() and add_rows.shape[-1] == width, "residual_rms_norm: bad add_rows")
+        check.fp32(add_rows=add_rows)
+        check(add_rows.is_contiguous() and add_rows.shape[-1] == width, "bad add_rows")
         period = add_rows.numel() // width
-    _require(weight.numel() == width, "residual_rms_norm: weight width")
+    check(weight.numel() == width, "weight width")
     L.call("iris_residual_rms_norm", L.ptr(residual), L.ptr(branch),
            L.dtype_code(branch.dtype) if branch is not None else L.F32, L.ptr(weight), L.ptr(add_rows), period, rows,
            width, float(eps), L.ptr(out), L.dtype_code(out.dtype), L.stream())
@@ -589,16 +598,16 @@ def gemv(
     with ``extra_bias`` (``[J, N]``) ``out[j] = y + extra_bias[j]`` (``out``: ``[J, B, N]``)."""
     n, k = weight.shape
     batch = x.shape[0]
-    _on_gpu(weight, x, bias, out, extra_bias)
-    _require(weight.dtype == torch.bfloat16 and weight.is_contiguous(), "gemv: BF16 contiguous weight")
-    _require(x.shape == (batch, k) and x.dtype == torch.float32 and x.is_contiguous(), "gemv: FP32 [B, K] input")
+    check = _Check("gemv", weight, x, bias, out, extra_bias)
+    check(weight.dtype == torch.bfloat16 and weight.is_contiguous(), "BF16 contiguous weight")
+    check(x.shape == (batch, k) and x.dtype == torch.float32 and x.is_contiguous(), "FP32 [B, K] input")
     n_extra = 0 if extra_bias is None else extra_bias.shape[0]
     expect = (n_extra, batch, n) if n_extra else (batch, n)
-    _require(tuple(out.shape) == expect and out.dtype == torch.float32 and out.is_contiguous(), "gemv: bad out")
+    check(tuple(out.shape) == expect and out.dtype == torch.float32 and out.is_contiguous(), "bad out")
     if bias is not None:
-        _require_fp32(bias=bias)
+        check.fp32(bias=bias)
     if extra_bias is not None:
-        _require_fp32(extra_bias=extra_bias)
+        check.fp32(extra_bias=extra_bias)
     L.call(
         "iris_gemv_bf16", L.ptr(weight), L.ptr(x), batch, n, k, L.ptr(bias), L.ptr(extra_bias), n_extra, L.ptr(out),
         L.ACT_SILU if in_silu else L.ACT_NONE, L.ACT_SILU if out_silu else L.ACT_NONE, L.stream(),
@@ -610,18 +619,18 @@ def patchify_embed(x, patch, pix_w, pix_b, pos_x, pos_y, norm_weight, eps, patch
     """Patch matrix for the patch embedder, the embedded pixel stream and its first norm
     (src/iris_metal/model.py:188-189, 208-210)."""
     batch, channels, height, width = x.shape
-    _on_gpu(x, patches, pixels, normed)
-    _require(channels in (3, 4) and x.dtype == torch.float32 and x.is_contiguous(),
-             "patchify_embed: FP32 [B, 3 or 4, H, W]")
-    _require_fp32(pix_w=pix_w, pix_b=pix_b, pos_x=pos_x, pos_y=pos_y, norm_weight=norm_weight)
-    _require(pix_w.shape == (PIXEL_WIDTH, channels), f"patchify_embed: pixel embedder weight must be [16, {channels}]")
+    check = _Check("patchify_embed", x, patches, pixels, normed)
+    check(channels in (3, 4) and x.dtype == torch.float32 and x.is_contiguous(),
+          "FP32 [B, 3 or 4, H, W]")
+    check.fp32(pix_w=pix_w, pix_b=pix_b, pos_x=pos_x, pos_y=pos_y, norm_weight=norm_weight)
+    check(pix_w.shape == (PIXEL_WIDTH, channels), f"pixel embedder weight must be [16, {channels}]")
     n_patches = (height // patch) * (width // patch)
-    _require(patches.dtype == torch.bfloat16 and patches.stride(-1) == 1
-             and patches.reshape(-1, patches.shape[-1]).shape[0] == batch * n_patches
-             and patches.shape[-1] >= channels * patch * patch,
-             "patchify_embed: patches must be BF16 [B*L, >= C*p*p]")
-    _require(pixels.numel() == normed.numel() == batch * height * width * PIXEL_WIDTH
-             and normed.dtype == torch.bfloat16, "patchify_embed: bad pixel buffers")
+    check(patches.dtype == torch.bfloat16 and patches.stride(-1) == 1
+          and patches.reshape(-1, patches.shape[-1]).shape[0] == batch * n_patches
+          and patches.shape[-1] >= channels * patch * patch,
+          "patches must be BF16 [B*L, >= C*p*p]")
+    check(pixels.numel() == normed.numel() == batch * height * width * PIXEL_WIDTH
+          and normed.dtype == torch.bfloat16, "bad pixel buffers")
     L.call(
         "iris_patchify_embed", L.ptr(x), batch, channels, height, width, patch, L.ptr(patches), patches.stride(-2),
         L.ptr(pix_w), L.ptr(pix_b),
@@ -634,12 +643,12 @@ def unpatchify_head(h, weight, bias, out, patch) -> torch.Tensor:
     """``out[b, c, y, x] = h[pixel] . weight[c] + bias[c]`` (src/iris_metal/model.py:214-217);
     3 output channels, or 1 for the depth head."""
     batch, channels, height, width = out.shape
-    _on_gpu(h, weight, bias, out)
-    _require(channels in (1, 3) and out.dtype == torch.float32 and out.is_contiguous(),
-             "unpatchify_head: FP32 output of 1 or 3 channels")
-    _require(h.dtype == torch.bfloat16 and h.is_contiguous(), "unpatchify_head: BF16 pixels")
-    _require_fp32(weight=weight, bias=bias)
-    _require(weight.shape == (channels, PIXEL_WIDTH) and bias.numel() == channels, "unpatchify_head: head shape")
+    check = _Check("unpatchify_head", h, weight, bias, out)
+    check(channels in (1, 3) and out.dtype == torch.float32 and out.is_contiguous(),
+          "FP32 output of 1 or 3 channels")
+    check(h.dtype == torch.bfloat16 and h.is_contiguous(), "BF16 pixels")
+    check.fp32(weight=weight, bias=bias)
+    check(weight.shape == (channels, PIXEL_WIDTH) and bias.numel() == channels, "head shape")
     L.call("iris_unpatchify_head", L.ptr(h), L.ptr(weight), L.ptr(bias), L.ptr(out), channels, batch, height, width,
            patch, L.stream())
     return out
@@ -647,9 +656,9 @@ def unpatchify_head(h, weight, bias, out, patch) -> torch.Tensor:
 
 def timestep_features(t: torch.Tensor, freqs: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     """``[cos | sin](t * freqs)`` (src/iris3b/nn/embeddings.py:41-45); ``out``: FP32 ``[B, 2*len(freqs)]``."""
-    _on_gpu(t, freqs, out)
-    _require_fp32(t=t, freqs=freqs, out=out)
-    _require(out.shape == (t.numel(), 2 * freqs.numel()), "timestep_features: bad out")
+    check = _Check("timestep_features", t, freqs, out)
+    check.fp32(t=t, freqs=freqs, out=out)
+    check(out.shape == (t.numel(), 2 * freqs.numel()), "bad out")
     L.call("iris_timestep_features", L.ptr(t), L.ptr(freqs), t.numel(), freqs.numel(), L.ptr(out), L.stream())
     return out
 
@@ -657,34 +666,34 @@ def timestep_features(t: torch.Tensor, freqs: torch.Tensor, out: torch.Tensor) -
 def copy_rows(src, dst, batch: int, rows: int, src_offset: int, src_batch_rows: int, dst_offset: int,
               dst_batch_rows: int) -> None:
     """``dst[b*dst_batch_rows + dst_offset + r] = src[b*src_batch_rows + src_offset + r]`` for FP32 rows."""
-    _on_gpu(src, dst)
-    _require_fp32(src=src, dst=dst)
+    check = _Check("copy_rows", src, dst)
+    check.fp32(src=src, dst=dst)
     width = src.shape[-1]
-    _require(dst.shape[-1] == width, "copy_rows: widths differ")
-    _require(src.numel() >= batch * src_batch_rows * width and dst.numel() >= batch * dst_batch_rows * width,
-             "copy_rows: buffers too small")
+    check(dst.shape[-1] == width, "widths differ")
+    check(src.numel() >= batch * src_batch_rows * width and dst.numel() >= batch * dst_batch_rows * width,
+          "buffers too small")
     L.call("iris_copy_rows", L.ptr(src), L.ptr(dst), batch, rows, width, src_batch_rows, src_offset, dst_batch_rows,
            dst_offset, L.stream())
 
 
 def silu_add_rows(x, t, rows_per_batch: int, out) -> None:
     """``out[r] = silu(x[r] + t[r // rows_per_batch])`` (src/iris_metal/model.py:207)."""
-    _on_gpu(x, t, out)
-    _require_fp32(x=x, t=t)
-    _require(out.shape == x.shape and out.is_contiguous(), "silu_add_rows: bad out")
+    check = _Check("silu_add_rows", x, t, out)
+    check.fp32(x=x, t=t)
+    check(out.shape == x.shape and out.is_contiguous(), "bad out")
     L.call("iris_silu_add_rows", L.ptr(x), L.ptr(t), x.shape[0], rows_per_batch, x.shape[1], L.ptr(out),
            L.dtype_code(out.dtype), L.stream())
 
 
 def flow_euler(x, v, sigma: float, sigma_next: float | None, x_next, clean) -> None:
     """Turbo Euler step in the reference's FP32 operation order (src/iris3b/sampling.py:129-135)."""
-    _on_gpu(x, v, x_next, clean)
+    check = _Check("flow_euler", x, v, x_next, clean)
     L.call("iris_flow_euler", L.ptr(x), L.ptr(v), x.numel(), float(sigma), float(sigma_next or 0.0),
            L.ptr(x_next) if sigma_next is not None else None, L.ptr(clean), L.stream())
 
 
 def dpm1_update(x, v, s: float, c_x: float, c_x0: float, out) -> None:
-    _on_gpu(x, v, out)
+    check = _Check("dpm1_update", x, v, out)
     L.call("iris_dpm1_update", L.ptr(x), L.ptr(v), x.numel(), float(s), float(c_x), float(c_x0), L.ptr(out),
            L.stream())
 
@@ -693,18 +702,18 @@ def dpm_update(x, v, x0_prev, s: float, c_x: float, c_x0: float, c_d: float, r0:
     """One FlowDPMSolver step (src/iris3b/flow/solver.py:90-109): first order when ``x0_prev``
     is None, else second order; ``x0_out`` receives this step's ``x0 = x - s*v``."""
     tensors = [t for t in (x, v, x0_prev, x_next, x0_out) if t is not None]
-    _on_gpu(*tensors)
-    _require(all(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == x.numel() for t in tensors),
-             "dpm_update needs contiguous FP32 tensors of one size")
+    check = _Check("dpm_update", *tensors)
+    check(all(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == x.numel() for t in tensors),
+          "needs contiguous FP32 tensors of one size")
     L.call("iris_dpm_update", L.ptr(x), L.ptr(v), L.ptr(x0_prev), x.numel(), float(s), float(c_x), float(c_x0),
            float(c_d), float(r0), L.ptr(x_next), L.ptr(x0_out), L.stream())
 
 
 def cfg_combine(v_uncond, v_cond, scale: float, out) -> None:
-    _on_gpu(v_uncond, v_cond, out)
+    check = _Check("cfg_combine", v_uncond, v_cond, out)
     L.call("iris_cfg_combine", L.ptr(v_uncond), L.ptr(v_cond), v_cond.numel(), float(scale), L.ptr(out), L.stream())
 
 
 def clamp(x, lo: float, hi: float, out) -> None:
-    _on_gpu(x, out)
+    check = _Check("clamp", x, out)
     L.call("iris_clamp", L.ptr(x), x.numel(), float(lo), float(hi), L.ptr(out), L.stream())

@@ -63,12 +63,14 @@ def _lam(t: float) -> float:
 @torch.no_grad()
 def dpm_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor | None = None, steps: int = 50,
                order: int = 2, shift: float = 1.0, cfg_scale: float = 1.0,
-               cfg_interval: tuple[float, float] = (0.0, 1.0), num_timesteps: int = 1000) -> torch.Tensor:
+               cfg_interval: tuple[float, float] = (0.0, 1.0), num_timesteps: int = 1000,
+               check=require_finite) -> torch.Tensor:
     """``FlowDPMSolver.sample`` (src/iris3b/flow/solver.py:111-141) with v-prediction: multistep
     DPM-Solver++ of order 1 or 2 (the order ramps up over the first steps and back to 1 at the
     end), classifier-free guidance over the batch ``cat([uncond, cond])`` for the steps whose
     start time lies inside ``cfg_interval`` (solver.py:58-74). Every update is one FP32 kernel
-    (``iris_dpm_update``) that also keeps the step's ``x0`` for the next one."""
+    (``iris_dpm_update``) that also keeps the step's ``x0`` for the next one. ``check`` sees the
+    final sample (the original route's ``require_finite``, src/iris_metal/pipeline.py:328)."""
     if order not in (1, 2):
         raise ValueError(f"order must be 1 or 2, got {order}")
     grid = time_grid(steps, shift)
@@ -107,12 +109,14 @@ def dpm_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor 
             K.dpm_update(x, v, x0_prev, s, t / s, (1.0 - t) * phi1, 0.5 * (1.0 - t) * phi1, h0 / h, x_next, x0)
         s_prev = s
         x, x_next = x_next, x
+    if check is not None:
+        check(x)
     return x
 
 
 def dpm1_sample(model, z: torch.Tensor, cond: torch.Tensor, uncond: torch.Tensor | None = None, steps: int = 20,
                 shift: float = 4.0, cfg_scale: float = 3.0, cfg_interval: tuple[float, float] = (0.0, 1.0),
-                num_timesteps: int = 1000) -> torch.Tensor:
+                num_timesteps: int = 1000, check=require_finite) -> torch.Tensor:
     """First-order ``FlowDPMSolver.sample`` (``dpm_sample`` with ``order=1``)."""
     return dpm_sample(model, z, cond, uncond, steps=steps, order=1, shift=shift, cfg_scale=cfg_scale,
-                      cfg_interval=cfg_interval, num_timesteps=num_timesteps)
+                      cfg_interval=cfg_interval, num_timesteps=num_timesteps, check=check)

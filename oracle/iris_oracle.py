@@ -12,13 +12,19 @@ follows. How each function is pinned (reference tests restated, golden vectors
 written by importing the unmodified ``iris3b.nn`` package, library routines,
 closed forms) is listed in the test files ``tests/test_oracle_*.py``.
 
-Parity status: every layer-level function is pinned. The block-level
-composition (``mmdit_block``, ``single_block``, ``pit_block``) and the
-top-level glue in ``forward`` are pinned by the reference's invariants (adaLN
-identity, zero-gate halving, sandwich-norm RMS, keep/drop equality,
-parameter count) and by library routines (unfold/fold); the reference's own
-``IrisDiT`` cannot be imported here (its config module needs omegaconf, which
-is absent), so their composed output is otherwise "parity unpinned".
+Parity status: every layer-level function is pinned by golden vectors of the
+unmodified ``iris3b.nn`` modules. The blocks ``mmdit_block``,
+``single_block`` and ``pit_block`` are pinned by golden vectors of the
+unmodified reference block modules (blocks/mmdit.py, single_stream.py,
+pit.py, loaded by file path) at the released topology and the tiny config.
+The reference's ``IrisDiT`` itself cannot be imported here (its config module
+needs omegaconf, which is absent), so the glue of ``forward`` that lives only
+in src/iris3b/models/dit.py:283-375 is "parity unpinned" beyond the
+reference's invariants (adaLN identity, keep/drop equality, zero head,
+parameter count) and unfold/fold: ``cond = silu(t_emb)``, the
+``y_pos_embedding`` add of ``embed_text``, the block loop's hand-over of
+``[text | image]`` rows, the ``silu(t_emb + s)`` re-fusion, and the
+``FinalLayer`` (RMSNorm then Linear).
 The downstream wrappers ``depth_forward`` and ``restore_tile`` are pinned by
 invariants of their own (``tests/test_tasks.py``): the zero fourth channel
 equals the three-channel model with the sliced embedders, and a head that

@@ -90,3 +90,32 @@ def test_engine_from_checkpoint_matches_engine_from_state_dict(tmp_path):
     t = torch.tensor([500.0]).cuda()
     text = torch.randn(1, RELEASED_TOPOLOGY.text_len, RELEASED_TOPOLOGY.hidden_size, generator=g).cuda()
     assert torch.equal(engine(x, t, text), direct(x, t, text))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_engine_from_checkpoint_matches_oracle(tmp_path, dtype):
+    """``load_engine`` on an FP32 and on a BF16 ``model.safetensors`` (the released Turbo
+    checkpoint is BF16) against the FP32 oracle over that file's own tensors, text through the
+    adapter (src/iris_metal/loading.py:20-77: Linear weights at the engine's BF16, every other
+    tensor widened to FP32)."""
+    from parity import check
+    from safetensors.torch import load_file
+
+    from oracle import iris_oracle as O
+
+    cfg = RELEASED_TOPOLOGY
+    state = {k: v.to(dtype) for k, v in synthetic_state_dict(cfg, seed=9).items()}
+    _checkpoint(tmp_path, state=state)
+    engine = loading.load_engine(tmp_path, device="cuda")
+    file_tensors = {k: v.float() for k, v in load_file(str(tmp_path / "model.safetensors")).items()}
+    assert all(v.dtype == dtype for v in load_file(str(tmp_path / "model.safetensors")).values())
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(2, 3, 32, 48, generator=g)
+    t = torch.tensor([1000.0, 625.0])
+    states = torch.randn(2, cfg.text_len, cfg.text_lap_num_layers, cfg.text_dim, generator=g)
+    mask = torch.zeros(2, cfg.text_len, dtype=torch.int64)
+    mask[0, :9], mask[1, :] = 1, 1
+    want = O.forward(file_tensors, cfg, x, t, y=states, y_mask=mask)
+    got = engine(x.cuda(), t.cuda(), engine.encode_text(states.cuda(), mask.cuda())).cpu()
+    check(got, want, f"checkpoint {dtype}")

@@ -15,7 +15,6 @@ from iris_mi355x.weights import save_state_dict, synthetic_state_dict
 from oracle import iris_oracle as O
 
 CFG = RELEASED_TOPOLOGY
-COS_MIN, MAX_REL = 0.999, 2e-2
 
 
 def depth_weights(seed=0):
@@ -127,11 +126,9 @@ def test_prefixed_view():
 
 # -- GPU: the HIP task engines against the oracle ----------------------------------------------
 def _check(got, want, label):
-    got, want = got.float().cpu().flatten(), want.float().flatten()
-    cos = F.cosine_similarity(got, want, dim=0).item()
-    max_rel = ((got - want).abs().max() / want.abs().max()).item()
-    print(f"{label}: cosine {cos:.6f} max-rel {max_rel:.3e}", flush=True)
-    assert cos >= COS_MIN and max_rel <= MAX_REL, (cos, max_rel)
+    from parity import check
+
+    check(got, want, label)
 
 
 @pytest.mark.gpu
