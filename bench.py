@@ -8,13 +8,25 @@ N(0, 1) prepared text tokens (the text adapter is outside the step, as in the re
 (recorded during the warm-up steps), the Euler update launched after it.
 
 Prints one JSON line. Besides the driver's fields it carries:
-- ``roofline``: the MFMA GEMM kernel's achieved TFLOP/s (algorithmic 2*M*N*K of each
-  launch, unpadded, over its HIP-event time on the launch stream) against the 2.5 PFLOP/s
-  dense BF16 peak, from a second timed pass of the same steps launched eagerly, so that every
-  GEMM launch can be bracketed by events (``eager_ms_per_step``);
-- ``cpu_baseline``: the FP32 CPU oracle timed on this host on one dual, one single and one
-  pixel block of the same 1024x1024 workload, composed into steps/s;
-- ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included);
+- ``roofline``: the dominant kernel, the trunk's SwiGLU w1/w3 GEMM (``gemm_kernel`` with the
+  SwiGLU epilogue, M x 2*6826 x 2560 per block), from a second timed pass of the same steps
+  launched eagerly so that every GEMM launch can be bracketed by HIP events on its stream
+  (``eager_ms_per_step``): ``achieved`` = algorithmic 2*M*N*K (unpadded) over the launches'
+  event time, against the 2.5 PFLOP/s dense BF16 peak; ``traffic`` = HBM bytes per launch of
+  that kernel from the committed counter summary
+  ``profiles/gemm_swiglu_4352x13696x2560_traffic.txt`` (null when it is absent);
+  ``gemm_all`` the same figures over every GEMM launch of the step;
+- ``cpu_baseline``: the FP32 CPU oracle timed on this host on one full forward of the same
+  workload plus its Euler update (``--cpu-turbo``: a whole 4-step Turbo sample instead);
+- ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included),
+  and ``cpu_turbo_4step_s`` beside it (measured with ``--cpu-turbo``, else four times the
+  timed CPU step, marked as such);
+- ``fused_ops``: the row kernels' bandwidth microbenchmark at [1, 4352, 2560] BF16 (achieved
+  GB/s on algorithmic bytes, buffers rotated past the Infinity Cache);
+- ``single_block``: one single-stream block at 1024x1024 (4352 joint tokens) on its own,
+  algorithmic TFLOP over its HIP-event time against the BF16 peak;
+- ``guided``: 20 first-order guided steps (scale 3.0) over two prompts, a batch of four
+  forwards per step (conditional N(0,1) tokens, zero unconditional tokens);
 - ``encode_text``: the once-per-prompt text adapter (12 encoder layers of 2560 per token,
   300 tokens of which 200 are real, batch 1) on the GPU, and the FP32 CPU oracle of the same
   prompt beside it (unless ``--no-cpu-baseline``).
@@ -107,7 +119,7 @@ class LaunchTimer:
             e.record()
             m = x.numel() // x.shape[-1]
             k = x.shape[-1] if x.shape[-1] != timer.patch_k else 3 * timer.cfg.patch_size ** 2
-            timer.records.append((s, e, timer.flops(m, weight.shape[0], k, swiglu)))
+            timer.records.append((s, e, timer.flops(m, weight.shape[0], k, swiglu), swiglu))
             return res
 
         def linear_grouped(xs, weights, biases, outs, swiglu=False):
@@ -118,67 +130,63 @@ class LaunchTimer:
             orig_grouped(xs, weights, biases, outs, swiglu)
             e.record()
             fl = sum(timer.flops(x.numel() // x.shape[-1], w.shape[0], x.shape[-1], swiglu) for x, w in zip(xs, weights))
-            timer.records.append((s, e, fl))
+            timer.records.append((s, e, fl, swiglu))
 
         K.linear, K.linear_grouped = linear, linear_grouped
 
-    def summary(self) -> tuple[float, float, int]:
-        ms = sum(s.elapsed_time(e) for s, e, _ in self.records)
-        fl = sum(f for _, _, f in self.records)
-        return fl, ms, len(self.records)
+    def summary(self, swiglu_only: bool = False) -> tuple[float, float, int]:
+        rows = [r for r in self.records if r[3] or not swiglu_only]
+        ms = sum(s.elapsed_time(e) for s, e, _, _ in rows)
+        fl = sum(f for _, _, f, _ in rows)
+        return fl, ms, len(rows)
 
 
-def cpu_baseline(height: int, width: int, n_text: int, seed: int = 0) -> dict:
-    """FP32 CPU oracle on one dual, one single and one pixel block of the workload."""
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_swiglu_4352x13696x2560_traffic.txt"
+
+
+def profiled_traffic(path: Path = TRAFFIC_PROFILE) -> float | None:
+    """HBM bytes per launch recorded by a counter summary (its ``traffic_bytes_per_launch:``
+    line), or None without one."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].strip().strip("`"))
+    return None
+
+
+def cpu_baseline(sd_cpu: dict, noise, text, turbo: bool) -> dict:
+    """The FP32 CPU oracle on this host's cores: one forward of the benchmarked workload plus
+    its Euler update (one Turbo step), or with ``turbo`` the whole 4-step Turbo sample."""
     import torch
-    from dataclasses import replace
 
     from iris_mi355x.config import IRIS_3B
-    from iris_mi355x.weights import synthetic_state_dict
     from oracle import iris_oracle as O
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    cfg = replace(IRIS_3B, depth=2, dual_depth=1, pixel=replace(IRIS_3B.pixel, depth=1))
-    sd = synthetic_state_dict(cfg, seed=seed)
-    p = cfg.patch_size
-    grid = (height // p, width // p)
-    L, D = grid[0] * grid[1], cfg.hidden_size
-    g = torch.Generator().manual_seed(seed)
-    s = torch.randn(1, L, D, generator=g)
-    text = torch.randn(1, n_text, D, generator=g)
-    cond = torch.randn(1, 1, D, generator=g)
-    img, txt, pix = O.rope_tables(cfg, grid, n_text)
-    tokens = torch.cat([text, s], dim=1)
-    pixels = torch.randn(L, p * p, cfg.pixel.hidden_size, generator=g)
-    cpix = torch.randn(L, D, generator=g)
-    blocks = {
-        "dual": lambda: O.mmdit_block(sd, cfg, 0, s, text, cond, img, txt),
-        "single": lambda: O.single_block(sd, cfg, 1, tokens, n_text, cond, img, txt),
-        "pixel": lambda: O.pit_block(sd, cfg, 0, pixels, cpix, pix, grid),
-    }
-    times = {}
-    with torch.no_grad():
-        for name, fn in blocks.items():  # median of 3 runs per block kind
-            runs = []
-            for _ in range(3):
-                t0 = time.perf_counter()
-                fn()
-                runs.append(time.perf_counter() - t0)
-            times[name] = sorted(runs)[1]
-    full = IRIS_3B
-    n_dual = full.dual_depth
-    step_s = n_dual * times["dual"] + (full.depth - n_dual) * times["single"] + full.pixel.depth * times["pixel"]
-    return {
-        "value": 1.0 / step_s,
-        "unit": "steps/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"FP32 oracle (torch CPU), median of 3 runs of one dual ({times['dual']:.2f}s), one single "
-                   f"({times['single']:.2f}s) and one pixel block ({times['pixel']:.2f}s) at {height}x{width}, "
-                   f"{n_text} text tokens, composed as {n_dual} dual + {full.depth - n_dual} single + "
-                   f"{full.pixel.depth} pixel blocks per step (embedders and head not counted)"),
-    }
+    cfg = IRIS_3B
+    noise, text = noise.float().cpu(), text.float().cpu()
+    with torch.no_grad():  # warm the thread pool and allocator on a small input
+        O.forward(sd_cpu, cfg, noise[:, :, :64, :64], torch.tensor([1000.0]), prepared_text=text)
+        if turbo:
+            t0 = time.perf_counter()
+            O.turbo_sample(lambda x, t: O.forward(sd_cpu, cfg, x, t, prepared_text=text), noise)
+            total = time.perf_counter() - t0
+            return {"value": 4.0 / total, "unit": "steps/s", "cores": threads, "kind": "port",
+                    "sample": f"one 4-step Turbo sample of the FP32 oracle (4 forwards + updates) at "
+                              f"{noise.shape[-2]}x{noise.shape[-1]}, {text.shape[1]} text tokens",
+                    "turbo_4step_s": total, "turbo_measured": True}
+        t0 = time.perf_counter()
+        v = O.forward(sd_cpu, cfg, noise, torch.tensor([1000.0]), prepared_text=text)
+        sigma, sigma_next = 1.0, 0.938
+        clean = noise - sigma * v
+        _ = (1 - sigma_next) * clean + sigma_next * (noise - (1 - sigma) * clean) / sigma
+        step_s = time.perf_counter() - t0
+    return {"value": 1.0 / step_s, "unit": "steps/s", "cores": threads, "kind": "port",
+            "sample": f"one Turbo step of the FP32 oracle (full forward, 24 trunk + 4 pixel blocks, and "
+                      f"the Euler update) at {noise.shape[-2]}x{noise.shape[-1]}, {text.shape[1]} text tokens",
+            "turbo_4step_s": 4.0 * step_s, "turbo_measured": False}
 
 
 def text_prompt(cfg, real: int = 200, seed: int = 2):
@@ -209,6 +217,58 @@ def cpu_encode_text(cfg, text_sd: dict) -> dict:
     return {"ms_per_prompt": 1000.0 * sorted(runs)[1], "cores": threads, "kind": "port"}
 
 
+def single_block_leg(engine, cfg, text, dev, reps: int = 10) -> dict:
+    """One single-stream block (the first, index ``dual_depth``) at 1024x1024 on its own: the
+    block's kernels re-run in place on the engine's workspace, timed by HIP events."""
+    import torch
+
+    from iris_mi355x import kernels as K
+
+    g = torch.Generator(device=dev).manual_seed(3)
+    grid = (64, 64)
+    x = torch.randn(1, grid[0] * grid[1], cfg.hidden_size, generator=g, device=dev)
+    t = torch.full((1,), 700.0, device=dev)
+    index = cfg.dual_depth
+    engine.block_forward(index, x, text, t, grid)
+    for _ in range(2):
+        engine.run_block()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        engine.run_block()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    n, d, hid = text.shape[1] + x.shape[1], cfg.hidden_size, cfg.mlp_hidden
+    qkvg = 2 * d + 2 * cfg.kv_heads * cfg.head_dim
+    flop = 2.0 * n * d * (qkvg + d + 2 * hid) + 2.0 * n * hid * d + 4.0 * n * n * d
+    del K
+    return {"block": index, "tokens": n, "ms": ms, "tflop": flop / 1e12,
+            "achieved_tflops": flop / (ms * 1e-3) / 1e12, "mfma_frac": flop / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+
+
+def guided_leg(engine, cfg, dev, size: int, n_text: int) -> dict:
+    """20 first-order guided steps, scale 3.0, two prompts: a batch of four forwards per step."""
+    import torch
+
+    from iris_mi355x.sampling import dpm1_sample
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    z = torch.randn(2, 3, size, size, generator=g, device=dev)
+    cond = torch.randn(2, n_text, cfg.hidden_size, generator=g, device=dev)
+    uncond = torch.zeros_like(cond)
+    dpm1_sample(engine, z, cond, uncond, steps=2, cfg_scale=3.0)  # records the batch-4 graph
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dpm1_sample(engine, z, cond, uncond, steps=20, cfg_scale=3.0)
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    step_tflop = step_flops(cfg, size, size, n_text, batch=4)["total"] / 1e12
+    return {"steps": 20, "prompts": 2, "batch": 4, "cfg_scale": 3.0, "s": total, "steps_per_s": 20 / total,
+            "step_tflop": step_tflop, "mfma_frac": step_tflop * 20 / total / BF16_PEAK_TFLOPS}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,7 +277,9 @@ def main() -> None:
     ap.add_argument("--size", type=int, default=1024)
     ap.add_argument("--text", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-turbo", action="store_true", help="time a whole 4-step Turbo sample on the CPU")
     ap.add_argument("--no-turbo", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the fused-op, single-block and guided legs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
@@ -233,16 +295,19 @@ def main() -> None:
     from iris_mi355x.sampling import TURBO_SIGMAS, turbo_sample
     from iris_mi355x.weights import synthetic_state_dict
 
+    def say(msg: str) -> None:
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cfg = IRIS_3B
-    print(f"[bench] drawing Iris-3B weights on {torch.cuda.get_device_name(dev)}", file=sys.stderr, flush=True)
+    say(f"drawing Iris-3B weights on {torch.cuda.get_device_name(dev)}")
     sd = synthetic_state_dict(cfg, seed=0, device=dev)
     engine = HipIris(cfg, sd, device=dev)  # graphs=True: the default path
-    text_sd = None
-    if not args.no_cpu_baseline:  # the adapter's weights, for its CPU oracle
-        text_sd = {k: v.cpu() for k, v in sd.items() if k.startswith(("y_embedder.", "y_pos_embedding"))}
+    sd_cpu = None
+    if not args.no_cpu_baseline:  # the same weights for the CPU oracle (12 GB of host memory)
+        sd_cpu = {k: v.cpu() for k, v in sd.items()}
     del sd
     torch.cuda.empty_cache()
 
@@ -267,11 +332,11 @@ def main() -> None:
         x, x_next = x_next, x
 
     warmup = max(args.warmup, 1)  # the first step records the forward's HIP graph
-    print("[bench] warmup", file=sys.stderr, flush=True)
+    say("warmup")
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
+    say(f"timing {args.steps} steps")
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(i)
@@ -285,7 +350,7 @@ def main() -> None:
         step(i)
     torch.cuda.synchronize()
     timer.enabled = True
-    print(f"[bench] timing {args.steps} eager steps (GEMM launch events)", file=sys.stderr, flush=True)
+    say(f"timing {args.steps} eager steps (GEMM launch events)")
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(i)
@@ -293,8 +358,18 @@ def main() -> None:
     eager_ms = 1000.0 * (time.perf_counter() - t0) / args.steps
     timer.enabled = False
     engine.graphs = True
-    gemm_flops, gemm_ms, gemm_launches = timer.summary()
-    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
+
+    def rate(swiglu_only: bool) -> dict:
+        fl, ms, launches = timer.summary(swiglu_only)
+        tflops = fl / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+        return {"achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tflops / BF16_PEAK_TFLOPS,
+                "launches": launches, "avg_launch_us": 1000.0 * ms / max(launches, 1),
+                "flop_per_launch": fl / max(launches, 1)}
+
+    roofline = {"bound": "mfma", "kernel": "gemm_kernel<256,256,...,SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
+                **rate(True), "traffic": profiled_traffic(),
+                "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
+    gemm_all = {"kernel": "gemm_kernel (every GEMM launch of the step)", **rate(False)}
 
     turbo_s = None
     if not args.no_turbo:
@@ -304,6 +379,18 @@ def main() -> None:
         turbo_sample(engine, noise, text)
         torch.cuda.synchronize()
         turbo_s = time.perf_counter() - t0
+
+    extras = {}
+    if not args.no_extras:
+        from iris_mi355x import microbench
+
+        say("fused-op bandwidth microbenchmark")
+        extras["fused_ops"] = {r["kernel"]: {"GB/s": r["GB/s"], "hbm_frac": r["hbm_frac"], "us": r["us"],
+                                             "bytes": r["bytes"]} for r in microbench.fused_ops()}
+        say("single-stream block at 1024x1024")
+        extras["single_block"] = single_block_leg(engine, cfg, text, dev)
+        say("guided sampling, 20 steps, batch 4")
+        extras["guided"] = guided_leg(engine, cfg, dev, size, n_text)
 
     # the once-per-prompt text adapter
     states, mask = text_prompt(cfg)
@@ -321,12 +408,11 @@ def main() -> None:
     del states_d, mask_d
 
     cpu = None
-    if not args.no_cpu_baseline:
-        print("[bench] CPU oracle of the text adapter", file=sys.stderr, flush=True)
-        encode["cpu_oracle"] = cpu_encode_text(cfg, text_sd)
-        del text_sd
-        print("[bench] CPU baseline (oracle, one block of each kind)", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(size, size, n_text)
+    if sd_cpu is not None:
+        say("CPU oracle of the text adapter")
+        encode["cpu_oracle"] = cpu_encode_text(cfg, sd_cpu)
+        say("CPU baseline: the FP32 oracle " + ("4-step Turbo sample" if args.cpu_turbo else "Turbo step"))
+        cpu = cpu_baseline(sd_cpu, noise, text, args.cpu_turbo)
 
     result = {
         "metric": "denoise steps/sec @1024^2 bf16 b=1 on 1 MI355X",
@@ -346,12 +432,13 @@ def main() -> None:
                    "pixel_blocks": cfg.pixel.depth, "parallelism": "single GPU"},
         "step_tflop": flops["total"] / 1e12,
         "mfma_frac_end_to_end": flops["total"] / (ms_per_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-        "roofline": {"bound": "mfma", "kernel": "gemm_kernel (all GEMM launches of the step)",
-                     "achieved": gemm_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": gemm_tflops / BF16_PEAK_TFLOPS, "traffic": None,
-                     "launches": gemm_launches, "avg_launch_us": 1000.0 * gemm_ms / max(gemm_launches, 1)},
+        "roofline": roofline,
+        "gemm_all": gemm_all,
         "turbo_4step_s": turbo_s,
+        "cpu_turbo_4step_s": None if cpu is None else cpu["turbo_4step_s"],
+        "cpu_turbo_4step_measured": None if cpu is None else cpu["turbo_measured"],
         "eager_ms_per_step": eager_ms,
+        **extras,
         "encode_text": encode,
         "cpu_baseline": cpu,
     }
