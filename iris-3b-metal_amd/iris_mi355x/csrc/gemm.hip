@@ -736,20 +736,24 @@ int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) 
 // Tile shape: the candidate with the least estimated time, rounds of workgroups over the
 // device's CUs (256 on MI355X; the last round costs as much as a full one) x tile area /
 // relative per-CU rate.
-// Rates were measured on the trunk and pixel-stage shapes (sustained runs): 256x256 with eight
-// 128x64 waves 1.09, with four 128x128 waves (register-staged refills) 1.05, 192x256 0.98,
-// 256x192 0.96, 128x128 at two workgroups per CU 0.9. The SwiGLU epilogue excludes the
-// 192-column tile.
+// The rates are what the candidates do inside the denoise step (alternating runs of the whole
+// step on one box, the only measurement that ranked them reliably: back-to-back runs of one
+// GEMM ranked them differently): 256x256 with four 128x128 waves and register-staged refills
+// (11) 1.12, with eight 128x64 waves and direct-to-LDS refills (1) 1.09 (SwiGLU w1/w3 265
+// against 248 us per launch; the step 0.56-0.68 ms slower), 192x256 0.98, 256x192 0.96, 128x128
+// at two workgroups per CU 0.9. Measured slower in the step and forced-only: the eight-wave
+// 4-stage ring of 32-deep K tiles (8; 282 us on SwiGLU, although 8% faster than tile 1 in
+// back-to-back runs), and four waves with direct-to-LDS refills (9, 10; 280-290 us).
+// The SwiGLU epilogue excludes the 192-column tiles, the SiLU epilogue the four-wave kernel.
 int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
   if (forced >= 0) return forced;
   struct Candidate {
     int tile, per_cu;
     double rate;
   };
-  // (tile 11 has tile 1's shape at a lower rate: forced only)
-  const Candidate candidates[] = {{1, 1, 1.09}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
+  const Candidate candidates[] = {{11, 1, 1.12}, {1, 1, 1.09}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
   const int cus = device_cus();
-  int best = 1;
+  int best = 11;
   double best_cost = 0.0;
   for (const Candidate& c : candidates) {
     const TileShape t = kTiles[c.tile];

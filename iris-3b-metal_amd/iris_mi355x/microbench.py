@@ -193,6 +193,7 @@ def main() -> None:
     p.add_argument("n", type=int)
     p.add_argument("k", type=int)
     p.add_argument("--tile", type=int, default=-1)
+    p.add_argument("--tiles", type=str, default=None, help="comma-separated tiles, each measured in turn")
     p.add_argument("--swiglu", action="store_true")
     p.add_argument("--rotate", type=int, default=1)
     p = sub.add_parser("attention")
@@ -209,7 +210,9 @@ def main() -> None:
     if args.cmd == "fused-ops":
         out = fused_ops()
     elif args.cmd == "gemm":
-        out = gemm(args.m, args.n, args.k, args.tile, swiglu=args.swiglu, rotate=args.rotate)
+        tiles = [int(t) for t in args.tiles.split(",")] if args.tiles else [args.tile]
+        out = [gemm(args.m, args.n, args.k, t, swiglu=args.swiglu, rotate=args.rotate) for t in tiles]
+        out = out[0] if len(out) == 1 else out
     elif args.cmd == "attention":
         out = attention(args.b, args.h, args.hkv, args.n, variant=args.variant)
     elif args.cmd == "encode-text":

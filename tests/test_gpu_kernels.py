@@ -282,6 +282,33 @@ def test_gemm_matches_fp32_reference(tile, mnk):
     close_bf16(out16, want - bias)
 
 
+@pytest.mark.parametrize("tile", [-1, 11, 1])
+@pytest.mark.parametrize("shape,swiglu", [((4352, 6400, 2560), False), ((4352, 13696, 2560), True),
+                                          ((4096, 16384, 2560), False)])
+def test_gemm_bf16_output_over_several_rounds(tile, shape, swiglu):
+    """BF16 output at trunk shapes of 425 to 1024 tiles of 256 x 256, more than one per CU: the
+    four-wave kernel runs persistently over its rounds for plain output (the next tile's first
+    K tile loaded while the current tile's output goes out), one tile per workgroup for SwiGLU;
+    checked on sampled rows against an FP32 product of the same BF16 operands."""
+    m, n, k = shape
+    g = torch.Generator(device=DEV).manual_seed(16)
+    a = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16)
+    _lib.call("iris_gemm_force_tile", tile)
+    try:
+        out = K.linear(a, w, swiglu=swiglu)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    rows = torch.cat([torch.arange(0, m, 61), torch.tensor([m - 1])])
+    prod = a[rows].float().cpu() @ w.float().cpu().T
+    if swiglu:
+        pairs = prod.reshape(len(rows), n // 64, 2, 32)
+        want = (F.silu(pairs[:, :, 0]) * pairs[:, :, 1]).reshape(len(rows), n // 2)
+    else:
+        want = prod
+    close_bf16(out[rows], want)
+
+
 @pytest.mark.parametrize("shape", [(4352, 6400, 2560), (4096, 16384, 2560)])
 def test_gemm_trunk_shapes(shape):
     m, n, k = shape
