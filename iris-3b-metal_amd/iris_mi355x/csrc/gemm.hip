@@ -436,48 +436,60 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
 }
 
 // Instruction order of one k-step of gemm_w4_kernel: an MFMA, then the next k-step's NR
-// fragment reads each followed by an MFMA, then W LDS writes and L global loads alternating
-// with MFMAs while they last, then the rest of the NM MFMAs.
+// fragment reads each followed by an MFMA, then W LDS writes and L global loads dealt over the
+// remaining MFMAs as evenly as they go (the first slots take one more of each when they do not
+// divide), then the MFMAs left over.
+template <int W, int L, int R, int... S>
+__device__ __forceinline__ void order_w4_slots(std::integer_sequence<int, S...>) {
+  (([] {
+     constexpr int w = W / R + (S < W % R ? 1 : 0);
+     constexpr int l = L / R + (S < L % R ? 1 : 0);
+     if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(0x200, w, 0);  // DS write
+     if constexpr (l > 0) __builtin_amdgcn_sched_group_barrier(0x020, l, 0);  // VMEM read
+     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
+   }()),
+   ...);
+}
+
 template <int NR, int NM, int W, int L>
 __device__ __forceinline__ void order_w4() {
-  static_assert(1 + NR + (W > L ? W : L) <= NM, "MFMAs per k-step");
+  constexpr int R = NM - 1 - NR;  // MFMAs after the fragment reads
+  static_assert(R > 0 && W <= 2 * R && L <= 2 * R, "MFMAs per k-step");
   __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   }
-  constexpr int X = W > L ? W : L;
-#pragma unroll
-  for (int i = 0; i < X; ++i) {
-    if (i < W) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-    if (i < L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-  }
-  if constexpr (NM - 1 - NR - X > 0) __builtin_amdgcn_sched_group_barrier(0x008, NM - 1 - NR - X, 0);
+  order_w4_slots<W, L, R>(std::make_integer_sequence<int, R>{});
 }
 
-// Four waves (one per SIMD), each owning a 128 x 128 block of a 256 x 256 tile, with register
-// staged refills: every wave loads its quarter of K tile t + 2 from global memory into
-// registers (16-byte loads that do not hold up the wave, unlike global_load_lds) while it
-// multiplies tile t, and writes tile t + 1, loaded one K tile earlier, into the free LDS
-// stage. A 128 x 128 block per wave reads half as many LDS bytes per MFMA as 128 x 64; the
-// accumulators live in the AGPRs. Inside each k-step the fragment reads of the next k-step,
-// then this k-step's share of the LDS writes and global loads, are spread between the MFMAs.
-template <int EPI, typename TC, bool PERSIST>
+// Four waves (one per SIMD) in a 2 x 2 grid over a BM x 256 tile, each owning a (BM/2) x 128
+// block (128 x 128 for BM = 256, 96 x 128 for BM = 192), with register-staged refills: every
+// wave loads its quarter of K tile t + 2 from global memory into registers (16-byte loads that
+// do not hold up the wave, unlike global_load_lds) while it multiplies tile t, and writes tile
+// t + 1, loaded one K tile earlier, into the free LDS stage. A 128-wide block per wave reads
+// fewer LDS bytes per MFMA than the eight-wave kernel's 128 x 64; the accumulators live in the
+// AGPRs. Inside each k-step the fragment reads of the next k-step, then this k-step's share of
+// the LDS writes and global loads, are spread between the MFMAs.
+template <int BM, int EPI, typename TC, bool PERSIST>
 __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
-  constexpr int BM = 256, BN = 256, BK = 64, NW = 4;
-  constexpr int WM = 128, WN = 128, FM = 4, FN = 4;
+  constexpr int BN = 256, BK = 64, NW = 4;
+  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
   constexpr int KS = BK / 16;
   constexpr int CPR = BK / 8;
   constexpr int RPL = 64 / CPR;                // rows per 1 KB wave load
-  constexpr int A_LOADS = BM / RPL / NW;       // 8
+  constexpr int A_LOADS = BM / RPL / NW;       // 8 (BM = 256) or 6 (BM = 192)
   constexpr int B_LOADS = BN / RPL / NW;       // 8
-  constexpr int LW = A_LOADS + B_LOADS;        // 16 loads of 16 bytes per lane per K tile
-  constexpr int LPS = LW / KS;                 // global loads per k-step
+  constexpr int LW = A_LOADS + B_LOADS;        // loads of 16 bytes per lane per K tile
   constexpr int NR = FN + FM, NM = FN * FM;    // fragment reads and MFMAs per k-step
   constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
-  static_assert(LW % KS == 0 && KS == 4, "loads per k-step");
+  static_assert(KS == 4 && BM % 64 == 0 && A_LOADS * RPL * NW == BM, "tile / wave split");
+  // the LW loads of a K tile are dealt over the 4 k-steps at G0..G3 (boundaries), its LDS
+  // writes over the first three at W0, W1
+  constexpr int G1 = (LW + 3) / 4, G2 = (2 * LW + 3) / 4, G3 = (3 * LW + 3) / 4;
+  constexpr int W0 = (LW + 2) / 3, W1 = (2 * LW + 2) / 3;
+  static_assert(W0 >= G1 && W1 >= G2, "a slot is written to LDS before it is reloaded");
   __shared__ __attribute__((aligned(1024))) bf16 lds[2 * STAGE];
 
   int cur_tile = persistent_tile(p, 0);
@@ -501,7 +513,7 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
       const bool is_a = i < A_LOADS;
-      const int r = (w * A_LOADS + (is_a ? i : i - A_LOADS)) * RPL + ld_r;
+      const int r = (is_a ? w * A_LOADS + i : w * B_LOADS + i - A_LOADS) * RPL + ld_r;
       off[i] = is_a ? min(jb.tm * BM + r, jb.m - 1) * static_cast<int>(p.lda) + 8 * (ld_p ^ swz<BK>(r))
                     : min(jb.tn * BN + r, N - 1) * static_cast<int>(p.ldb) + 8 * (ld_p ^ swz<BK>(r));
     }
@@ -567,7 +579,6 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
   // four k-steps load a quarter of tile t + 2 each into slots already written. The barrier
   // before the last k-step publishes the writes and retires stage t % 2. Past the end the
   // loads repeat the last K tile; nothing writes them to LDS.
-  constexpr int W0 = 6, W1 = 11;  // LDS-write split points
   const int KT = p.k / BK;
   gload(0, 0, LW);
   for (int round = 0;; ++round) {
@@ -583,30 +594,30 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
     // k-step 0
     read_frags(S, 1, 1);
     lwrite(S ^ 1, 0, W0);
-    gload(t2, 0, LPS);
+    gload(t2, 0, G1);
     mfmas(0);
-    order_w4<NR, NM, W0, LPS>();
+    order_w4<NR, NM, W0, G1>();
     // k-step 1
     read_frags(S, 2, 0);
     lwrite(S ^ 1, W0, W1);
-    gload(t2, LPS, 2 * LPS);
+    gload(t2, G1, G2);
     mfmas(1);
-    order_w4<NR, NM, W1 - W0, LPS>();
+    order_w4<NR, NM, W1 - W0, G2 - G1>();
     // k-step 2
     read_frags(S, 3, 1);
     lwrite(S ^ 1, W1, LW);
-    gload(t2, 2 * LPS, 3 * LPS);
+    gload(t2, G2, G3);
     mfmas(0);
-    order_w4<NR, NM, LW - W1, LPS>();
+    order_w4<NR, NM, LW - W1, G3 - G2>();
     // k-step 3: publish tile t + 1, then read its first fragments behind the last MFMAs
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes and reads are done
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(S ^ 1, 0, 0);
-    gload(t2, 3 * LPS, LW);
+    gload(t2, G3, LW);
     mfmas(1);
-    order_w4<NR, NM, 0, LPS>();
+    order_w4<NR, NM, 0, LW - G3>();
   };
   int t = 0;
   for (; t + 2 < KT; t += 2) {
@@ -680,21 +691,22 @@ int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
 // loaded while the current tile is stored); the SwiGLU and FP32 epilogues keep one tile per
 // workgroup, since the register allocator spills inside the K loop when their epilogue shares
 // the persistent loop with it.
+template <int BM>
 int launch_w4(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   if (epilogue == IRIS_EPI_SILU) return fail(IRIS_E_UNSUPPORTED, "gemm: the four-wave tile has no SiLU epilogue");
   const int cus = device_cus();
   const dim3 all(args.total_tiles);
   if (epilogue == IRIS_EPI_SILU_MUL) {
     if (c_dtype == IRIS_BF16)
-      gemm_w4_kernel<IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, 0, stream>>>(args);
+      gemm_w4_kernel<BM, IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, 0, stream>>>(args);
     else
-      gemm_w4_kernel<IRIS_EPI_SILU_MUL, float, false><<<all, 256, 0, stream>>>(args);
+      gemm_w4_kernel<BM, IRIS_EPI_SILU_MUL, float, false><<<all, 256, 0, stream>>>(args);
   } else {
     if (c_dtype == IRIS_BF16)
-      gemm_w4_kernel<IRIS_EPI_NONE, bf16, true><<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, 0,
-                                                   stream>>>(args);
+      gemm_w4_kernel<BM, IRIS_EPI_NONE, bf16, true><<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, 0,
+                                                       stream>>>(args);
     else
-      gemm_w4_kernel<IRIS_EPI_NONE, float, false><<<all, 256, 0, stream>>>(args);
+      gemm_w4_kernel<BM, IRIS_EPI_NONE, float, false><<<all, 256, 0, stream>>>(args);
   }
   return check_launch("gemm_bf16");
 }
@@ -719,6 +731,7 @@ constexpr TileShape kTiles[] = {
     {256, 256, 64, 2, 2, 2, 1},  // 9: one wave per SIMD
     {256, 256, 64, 2, 2, 2, 2},  // 10
     {256, 256, 64, 2, 2, 2, 1, true},  // 11: gemm_w4_kernel
+    {192, 256, 64, 2, 2, 2, 1, true},  // 12: gemm_w4_kernel, 96 x 128 per wave
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -726,8 +739,8 @@ template <int I>
 int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   constexpr TileShape t = kTiles[I];
   if constexpr (t.w4) {
-    static_assert(t.bm == 256 && t.bn == 256 && t.bk == 64, "gemm_w4_kernel tile");
-    return launch_w4(args, c_dtype, epilogue, stream);
+    static_assert((t.bm == 256 || t.bm == 192) && t.bn == 256 && t.bk == 64, "gemm_w4_kernel tile");
+    return launch_w4<t.bm>(args, c_dtype, epilogue, stream);
   } else {
     return launch_tile<t.bm, t.bn, t.bk, t.stages, t.wgm, t.wgn, t.parts>(args, c_dtype, epilogue, stream);
   }
@@ -740,10 +753,13 @@ int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) 
 // step on one box, the only measurement that ranked them reliably: back-to-back runs of one
 // GEMM ranked them differently): 256x256 with four 128x128 waves and register-staged refills
 // (11) 1.12, with eight 128x64 waves and direct-to-LDS refills (1) 1.09 (SwiGLU w1/w3 265
-// against 248 us per launch; the step 0.56-0.68 ms slower), 192x256 0.98, 256x192 0.96, 128x128
-// at two workgroups per CU 0.9. Measured slower in the step and forced-only: the eight-wave
-// 4-stage ring of 32-deep K tiles (8; 282 us on SwiGLU, although 8% faster than tile 1 in
-// back-to-back runs), and four waves with direct-to-LDS refills (9, 10; 280-290 us).
+// against 248 us per launch; the step 0.56-0.68 ms slower); 192x256 with four 96x128 waves
+// (12) 1.04 against 0.98 for eight 96x64 waves (5) (proj and w2: the step 0.47 ms faster; at
+// 1.08 the model would also move SwiGLU onto it, 4 us per launch slower than tile 11);
+// 256x192 0.96, 128x128 at two workgroups per CU 0.9. Measured slower in the step and
+// forced-only: the eight-wave 4-stage ring of 32-deep K tiles (8; 282 us on SwiGLU, although
+// 8% faster than tile 1 in back-to-back runs), and four waves with direct-to-LDS refills
+// (9, 10; 280-290 us).
 // The SwiGLU epilogue excludes the 192-column tiles, the SiLU epilogue the four-wave kernel.
 int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
   if (forced >= 0) return forced;
@@ -751,7 +767,8 @@ int pick_tile(const int* m, int groups, int n, int epilogue, int forced) {
     int tile, per_cu;
     double rate;
   };
-  const Candidate candidates[] = {{11, 1, 1.12}, {1, 1, 1.09}, {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
+  const Candidate candidates[] = {{11, 1, 1.12}, {12, 1, 1.04}, {1, 1, 1.09},
+                                   {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
   const int cus = device_cus();
   int best = 11;
   double best_cost = 0.0;
@@ -830,7 +847,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   args.total_tiles = begin;
   if (begin == 0) return IRIS_OK;
   IRIS_REQUIRE(epilogue != IRIS_EPI_SILU_MUL || shape.swiglu(), "gemm: tile %dx%d has no SwiGLU epilogue", bm, bn);
-  static_assert(kNumTiles == 12, "one case per tile shape");
+  static_assert(kNumTiles == 13, "one case per tile shape");
   switch (tile) {
 #define IRIS_TILE_CASE(I) \
   case I:                 \
@@ -847,6 +864,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
     IRIS_TILE_CASE(9)
     IRIS_TILE_CASE(10)
     IRIS_TILE_CASE(11)
+    IRIS_TILE_CASE(12)
 #undef IRIS_TILE_CASE
     default:
       return fail(IRIS_E_INVALID, "gemm: no tile shape %d", tile);
