@@ -15,7 +15,8 @@ Prints one JSON line. Besides the driver's fields it carries:
   event time, against the 2.5 PFLOP/s dense BF16 peak; ``traffic`` = HBM bytes per launch of
   that kernel from the committed counter summary
   ``profiles/gemm_swiglu_4352x13696x2560_traffic.txt`` (null when it is absent);
-  ``gemm_all`` the same figures over every GEMM launch of the step;
+  ``gemm_all`` the same figures over every GEMM launch of the step, ``attention`` and
+  ``attention_pixel`` over the trunk's and the pixel stage's attention launches (4*N^2*H*128);
 - ``cpu_baseline``: the FP32 CPU oracle timed on this host on one full forward of the same
   workload plus its Euler update (``--cpu-turbo``: a whole 4-step Turbo sample instead);
 - ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included),
@@ -93,6 +94,7 @@ class LaunchTimer:
         self.cfg = cfg
         self.hidden_pad = hidden_pad
         self.records: list = []
+        self.attention: list = []  # (start, end, flop, query heads) per attention launch
         self.enabled = False
 
     def flops(self, m: int, n: int, k: int, swiglu: bool) -> float:
@@ -132,13 +134,34 @@ class LaunchTimer:
             fl = sum(timer.flops(x.numel() // x.shape[-1], w.shape[0], x.shape[-1], swiglu) for x, w in zip(xs, weights))
             timer.records.append((s, e, fl, swiglu))
 
-        K.linear, K.linear_grouped = linear, linear_grouped
+        orig_attn = K.flash_attention
+
+        def flash_attention(q, k, vt, n, out0, out1, *args, **kwargs):
+            if not timer.enabled:
+                return orig_attn(q, k, vt, n, out0, out1, *args, **kwargs)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            orig_attn(q, k, vt, n, out0, out1, *args, **kwargs)
+            e.record()
+            timer.attention.append((s, e, 4.0 * q.shape[0] * q.shape[1] * n * n * q.shape[3], q.shape[1]))
+
+        K.linear, K.linear_grouped, K.flash_attention = linear, linear_grouped, flash_attention
 
     def summary(self, swiglu_only: bool = False) -> tuple[float, float, int]:
         rows = [r for r in self.records if r[3] or not swiglu_only]
         ms = sum(s.elapsed_time(e) for s, e, _, _ in rows)
         fl = sum(f for _, _, f, _ in rows)
         return fl, ms, len(rows)
+
+
+    def attention_summary(self, heads: int) -> dict:
+        rows = [r for r in self.attention if r[3] == heads]
+        ms = sum(s.elapsed_time(e) for s, e, _, _ in rows)
+        fl = sum(f for _, _, f, _ in rows)
+        tflops = fl / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+        return {"achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tflops / BF16_PEAK_TFLOPS,
+                "launches": len(rows), "avg_launch_us": 1000.0 * ms / max(len(rows), 1),
+                "flop_per_launch": fl / max(len(rows), 1)}
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_swiglu_4352x13696x2560_traffic.txt"
@@ -370,6 +393,10 @@ def main() -> None:
                 **rate(True), "traffic": profiled_traffic(),
                 "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
     gemm_all = {"kernel": "gemm_kernel (every GEMM launch of the step)", **rate(False)}
+    attention = {"kernel": "flash_attn_kernel, trunk joint attention (20 query / 5 K/V heads)",
+                 **timer.attention_summary(cfg.num_heads)}
+    attention_pixel = {"kernel": "flash_attn_kernel, pixel-stage attention (10 heads)",
+                       **timer.attention_summary(cfg.pixel.num_heads)}
 
     turbo_s = None
     if not args.no_turbo:
@@ -434,6 +461,8 @@ def main() -> None:
         "mfma_frac_end_to_end": flops["total"] / (ms_per_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "roofline": roofline,
         "gemm_all": gemm_all,
+        "attention": attention,
+        "attention_pixel": attention_pixel,
         "turbo_4step_s": turbo_s,
         "cpu_turbo_4step_s": None if cpu is None else cpu["turbo_4step_s"],
         "cpu_turbo_4step_measured": None if cpu is None else cpu["turbo_measured"],

@@ -28,8 +28,6 @@ namespace iris {
 namespace {
 
 constexpr int kHd = 128;
-// word 3 of a raw buffer resource on gfx9-family GPUs (32-bit dwords, no swizzle)
-constexpr int kBufferFlags = 0x00020000;
 
 struct AttnArgs {
   const bf16* q;
@@ -133,7 +131,7 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int g = lane >> 5;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS targets stay scalar
   const int group = p.heads / p.kv_heads;
   const int h = kvh * group + hg * p.hpw + (w % p.hpw);
   const int q0 = qblk * p.rows_per_wg + (w / p.hpw) * 32 * QB;
@@ -161,24 +159,27 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
     const int vd = (w * LOADS + j) * VRPL + lane / VCPR;
     v_off[j] = vd * static_cast<int>(n_pad) + 8 * ((lane % VCPR) ^ swz<VCPR>(vd));
   }
-  auto issue = [&](int t, int stage) {
-    if (NW != 4 && w >= 4) return;  // (wave-uniform: the first four waves fetch)
-    bf16* kl = lds + stage * STAGE;
-    bf16* vl = kl + TILE;
-    const bf16* kt = kh + static_cast<long>(t) * KVT * kHd;
-    const bf16* vt = vh + static_cast<long>(t) * KVT;
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      __builtin_amdgcn_global_load_lds((const void*)(kt + k_off[j]), (void*)(kl + (w * LOADS + j) * 512), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vt + v_off[j]), (void*)(vl + (w * LOADS + j) * 512), 16, 0, 0);
-    }
-  };
-  // register-staged path: lane l's 16 bytes of load j land at byte 16 l of the same 1 KB blocks
-  bf16x8 kreg[LOADS], vreg[LOADS];
+  // K and V^T of this (batch, K/V head) as buffer resources: a 32-bit VGPR byte offset per lane,
+  // the tile position in an SGPR (n_pad < 2^23 keeps the offsets in range)
   const __amdgpu_buffer_rsrc_t rk =
       __builtin_amdgcn_make_buffer_rsrc((void*)kh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc((void*)vh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
+  // ring path: buffer loads straight into LDS. (global_load_lds with 64-bit VGPR addresses made
+  // the compiler wait for every outstanding load, the ring's prefetch included, before the first
+  // MFMA of each tile.)
+  auto issue = [&](int t, int stage) {
+    if (NW != 4 && w >= 4) return;  // (wave-uniform: the first four waves fetch)
+    bf16* kl = lds + stage * STAGE;
+    bf16* vl = kl + TILE;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      buffer_load_lds16(rk, kl + (w * LOADS + j) * 512, k_off[j] * 2, t * KVT * kHd * 2);
+      buffer_load_lds16(rv, vl + (w * LOADS + j) * 512, v_off[j] * 2, t * KVT * 2);
+    }
+  };
+  // register-staged path: lane l's 16 bytes of load j land at byte 16 l of the same 1 KB blocks
+  bf16x8 kreg[LOADS], vreg[LOADS];
   auto gload = [&](int t) {
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
@@ -241,20 +242,36 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) s[kb][qb] = f32x16{};
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      bf16x8 kf[KB];
+    // K fragments in a ring of KD k-steps: each MFMA's operand was requested KD - 1 MFMAs of
+    // this wave earlier, so the LDS latency hides behind them
+    constexpr int KD = KB == 1 ? 4 : 2;
+    bf16x8 kf[KD][KB];
+    auto read_k = [&](int st, int slot) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const int r = kb * 32 + l32;
-        kf[kb] = *reinterpret_cast<const bf16x8*>(kl + r * kHd + 8 * ((2 * st + g) ^ swz<16>(r)));
+        kf[slot][kb] = *reinterpret_cast<const bf16x8*>(kl + r * kHd + 8 * ((2 * st + g) ^ swz<16>(r)));
       }
+    };
+#pragma unroll
+    for (int st = 0; st < KD; ++st) read_k(st, st);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
-          s[kb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb], qf[qb][st], s[kb][qb], 0, 0, 0);
+          s[kb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st % KD][kb], qf[qb][st], s[kb][qb], 0, 0, 0);
+      if (st + KD < 8) read_k(st + KD, st % KD);
     }
+    // keep that order (the scheduler would otherwise sink the reads to one MFMA ahead)
+    __builtin_amdgcn_sched_group_barrier(0x100, KD * KB, 0);  // DS read
+#pragma unroll
+    for (int st = 0; st + KD < 8; ++st) {
+      __builtin_amdgcn_sched_group_barrier(0x008, KB * QB, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, KB, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, KD * KB * QB, 0);
 
     const int kv0 = t * KVT;
     if constexpr (MASKED) {
@@ -343,21 +360,33 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
 
     // O^T[d, q] += V^T[d, keys] P^T[keys, q], 16 keys per MFMA step: k-index g*8 + m is
     // key kb*32 + 16 jj + 8 (m / 4) + 4 g + m % 4 for both operands.
+    // V^T fragments in a ring of VD steps, as the K fragments above
+    constexpr int NV = KB * 2 * 4;  // (kb, jj, db) steps
+    constexpr int VD = 4;
+    bf16x8 vfr[VD];
+    auto read_v = [&](int i, int slot) {
+      const int kb = i / 8, jj = (i / 4) % 2, db = i % 4;
+      const int c = 4 * kb + 2 * jj + g;
+      const int d = db * 32 + l32;
+      vfr[slot] = *reinterpret_cast<const bf16x8*>(vl + d * KVT + 8 * (c ^ swz<VCPR>(d)));
+    };
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
+    for (int i = 0; i < VD; ++i) read_v(i, i);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int c = 4 * kb + 2 * jj + g;
+    for (int i = 0; i < NV; ++i) {
+      const int kb = i / 8, jj = (i / 4) % 2, db = i % 4;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const int d = db * 32 + l32;
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vl + d * KVT + 8 * (c ^ swz<VCPR>(d)));
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][jj][qb], o[db][qb], 0, 0, 0);
-        }
-      }
+      for (int qb = 0; qb < QB; ++qb)
+        o[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[i % VD], pf[kb][jj][qb], o[db][qb], 0, 0, 0);
+      if (i + VD < NV) read_v(i + VD, i % VD);
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, VD, 0);
+#pragma unroll
+    for (int i = 0; i + VD < NV; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, QB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, VD * QB, 0);
     if constexpr (STAGED) {
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): tile t + 1 written, tile t's reads done
       __builtin_amdgcn_s_barrier();

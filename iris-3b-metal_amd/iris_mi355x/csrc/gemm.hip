@@ -23,8 +23,6 @@ namespace iris {
 namespace {
 
 constexpr int kBK = 64;
-// word 3 of a raw buffer resource on gfx9-family GPUs (32-bit dwords, no swizzle)
-constexpr int kBufferFlags = 0x00020000;
 
 struct GemmGroup {
   const bf16* a;
@@ -54,14 +52,6 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (lds wave-uniform). (A
-// non-template device function: the host compilation pass never instantiates it, which it would
-// reject for the LDS address-space cast, and the kernels calling it keep their launch stubs.)
-__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, bf16* lds, int voffset, int soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0,
-                                           0);
 }
 
 // Same, and also all LDS reads of this wave (lgkmcnt = 0).

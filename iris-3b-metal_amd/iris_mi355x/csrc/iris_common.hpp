@@ -127,4 +127,17 @@ __device__ __forceinline__ int xcd_remap(int wg, int total) {
   return xcd * base + (xcd < rem ? xcd : rem) + local;
 }
 
+// Raw buffer resources: word 3 of a gfx9-family buffer descriptor (32-bit dwords, no swizzle).
+// A buffer load takes one 32-bit VGPR byte offset and an SGPR offset, and reads past the
+// resource's size return zeros instead of faulting.
+constexpr int kBufferFlags = 0x00020000;
+
+// 16 bytes per lane from a buffer straight into LDS at lds + 16 * lane (lds wave-uniform). (A
+// non-template device function: the host compilation pass never instantiates it, which it would
+// reject for the LDS address-space cast, and the kernels calling it keep their launch stubs.)
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, bf16* lds, int voffset, int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0,
+                                           0);
+}
+
 }  // namespace iris
