@@ -171,8 +171,9 @@ int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int
 
 /* Tuning hook for the benchmark sweep and the tile tests: force the GEMM tile of later
  * iris_gemm_bf16* calls made by the calling thread (an index into the tile table of gemm.hip:
- * 0-10 eight- and four-wave tiles of 256x256, 256x192, 192x256 and 128x128; 11 the four-wave
- * 128x128-per-wave kernel, never chosen automatically) or restore the automatic choice (-1).
+ * 0-10 tiles of 256x256, 256x192, 192x256 and 128x128 for the kernel with direct-to-LDS
+ * refills; 11 and 12 the four-wave kernel with register-staged refills at 256x256 and 192x256,
+ * the automatic choice for most shapes) or restore the automatic choice (-1).
  * The setting is per thread. No counterpart in the reference. */
 int iris_gemm_force_tile(int tile);
 

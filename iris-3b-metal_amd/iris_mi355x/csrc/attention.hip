@@ -4,9 +4,9 @@
 //
 // Workgroup = 4 waves sharing one K/V head: with G = heads / kv_heads query heads per K/V
 // head, a workgroup serves hpw = min(G, 4) of them and 32 * QB * 4 / hpw query rows, one
-// wave per (query head, 32*QB-row block). K/V tiles of KVT keys go global -> LDS with
-// global_load_lds_dwordx4 (no register staging) into a ring of STAGES buffers, and are
-// read by all four waves.
+// wave per (query head, 32*QB-row block). K/V tiles of KVT keys go global -> LDS by
+// buffer_load_dwordx4 ... lds (no register staging) into a ring of STAGES buffers, and are
+// read by all the workgroup's waves.
 //
 // Each wave computes S^T = K Q^T (v_mfma_f32_32x32x16_bf16, K fragments from LDS, Q
 // fragments held in registers), so every lane owns one query column and half of the keys
@@ -92,16 +92,15 @@ __device__ __forceinline__ void store_row(const AttnArgs& p, const f32x16 (&o)[4
   }
 }
 
-// STAGED: K/V tiles travel global -> registers (16-byte buffer loads, which do not hold up the
-// wave as global_load_lds does) -> LDS (ds_write_b128) through two LDS stages: tile t + 1 is
-// written while tile t is multiplied, tile t + 2 is loaded meanwhile. Otherwise a ring of
-// STAGES tiles filled by global_load_lds.
+// STAGED: K/V tiles travel global -> registers (16-byte buffer loads) -> LDS (ds_write_b128)
+// through two LDS stages: tile t + 1 is written while tile t is multiplied, tile t + 2 is
+// loaded meanwhile. Otherwise a ring of STAGES tiles filled by buffer loads straight into LDS.
 // MASKED: query q attends key j < n iff key_mask[b, j] != 0 or j == q. A tile can then hold no
 // key of some query; its running max stays -inf and the exponentials use 0 in its place, so
 // they are exactly 0 instead of NaN.
 // NW: waves per workgroup; with NW = 12 (one workgroup per CU, three waves per SIMD: four query
 // heads x three 32-row blocks) the first four waves fetch the K/V tiles that all twelve share,
-// a third of the fetches of three 4-wave workgroups (global_load_lds ring only).
+// a third of the fetches of three 4-wave workgroups (ring only).
 template <int QB, int STAGES, int KVT, bool STAGED, bool MASKED = false, int NW = 4>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 12 ? 3 : (QB == 1 ? 2 : 1)))) void
 flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
@@ -114,7 +113,7 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
   constexpr int VRPL = 64 / VCPR;  // V^T rows per 1 KB load
   static_assert(KVT == 32 || KVT == 64, "K/V tile of 32 or 64 keys");
   static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64 && (!STAGED || STAGES == 2), "pipeline depth");
-  static_assert(NW == 4 || (NW == 12 && !STAGED), "twelve-wave workgroups use the global_load_lds ring");
+  static_assert(NW == 4 || (NW == 12 && !STAGED), "twelve-wave workgroups use the LDS ring");
   __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
   // logical workgroup: (b, kv head, head group) major, query block minor; the XCD remap keeps
@@ -410,7 +409,7 @@ struct Variant {
   int nw = 4;
 };
 // 0: 32 query rows per wave, 64-key tiles staged through registers; 1: the same with 32-key
-// tiles; 2: 64-key tiles, 2-stage global_load_lds ring; 3: 32-key tiles, 3-stage ring; 4: 32-key
+// tiles; 2: 64-key tiles, 2-stage ring; 3: 32-key tiles, 3-stage ring; 4: 32-key
 // tiles in a 3-stage ring shared by twelve waves (four query heads x three row blocks).
 // (Measured and dropped: twelve-wave rings of 4 and 6 stages (1-2% slower than 3), eight of the
 // twelve waves fetching instead of four (2% slower), 64-key tiles at twelve waves (spills); an eight-wave ping-pong of MFMA and softmax phases, 1.8x slower at the
@@ -471,7 +470,7 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   // are at least 80% full, 9-11% faster than variant 1 there; else 32-key tiles staged through
   // registers in three 4-wave workgroups per CU (variant 1: 168 VGPRs; small grids spread
   // over more CUs). One query head per K/V head (the pixel stage): 64-key tiles in a
-  // global_load_lds ring. Each measured fastest at its shapes.
+  // 2-stage ring. Each measured fastest at its shapes.
   int variant = g_attn_variant;
   if (variant < 0) {
     variant = group >= 4 ? 1 : 2;

@@ -63,7 +63,7 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 
 // LDS layout: each operand tile is BM (or BN) rows of BK bf16, unpadded; the 16-byte chunk c
 // of row r is stored at chunk c ^ swz(r) so that the 16 rows read by one ds_read_b128 phase
-// cover all 64 banks. Tiles are filled by global_load_lds_dwordx4, which writes lane i's
+// cover all 64 banks. Tiles are filled by buffer_load_dwordx4 ... lds, which writes lane i's
 // 16 bytes at LDS base + 16 i: each lane therefore fetches the global chunk that belongs
 // at its LDS position.
 template <int BK>
