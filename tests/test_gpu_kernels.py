@@ -40,7 +40,7 @@ def close_attention(got, want, rel_l2=4e-3):
 
 
 # -- rows ------------------------------------------------------------------------------
-@pytest.mark.parametrize("shape", [(1, 4352, 2560), (2, 37, 256), (3, 7, 384)])
+@pytest.mark.parametrize("shape", [(1, 4352, 2560), (2, 37, 256), (3, 7, 384), (2, 64, 384)])
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
 def test_rms_norm_modulate(shape, x_dtype):
     b, n, d = shape
@@ -72,7 +72,7 @@ def test_gated_residual_rms_norm(branch_dtype):
     torch.testing.assert_close(r.cpu(), want, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("shape", [(1, 4352, 2560), (2, 37, 256)])
+@pytest.mark.parametrize("shape", [(1, 4352, 2560), (2, 37, 256), (2, 64, 384)])
 def test_gated_residual_fused_with_next_norm_modulate(shape):
     b, n, d = shape
     g = gen(22)
