@@ -17,8 +17,9 @@
 // middle two 4-key quads of every 16 keys swapped, so each V^T fragment is one 16-byte read.
 //
 // The softmax is VALU work beside the MFMAs, so it is kept short: exponentials are the bare
-// v_exp_f32 (results below 2^-126 flush to zero, far under bf16 resolution of P), and the
-// running output is rescaled only when the running max of some query column moved.
+// v_exp_f32 of one fma (s * scale * log2(e) - max, a single rounding written out, so that every
+// variant rounds alike; results below 2^-126 flush to zero, far under bf16 resolution of P),
+// and the running output is rescaled only when the running max of some query column moved.
 //
 // LDS: K rows are 256 bytes, V^T rows 2*KVT bytes; chunk c of row r is stored at chunk
 // c ^ swz(r) so the 16-lane phases of ds_read_b128 hit 64 distinct banks.
@@ -324,7 +325,7 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
         for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            pf[kb][jj][qb][e] = from_f32<bf16>(__builtin_amdgcn_exp2f(s[kb][qb][8 * jj + e] * sl2 - m));
+            pf[kb][jj][qb][e] = from_f32<bf16>(__builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][8 * jj + e], sl2, -m)));
 #pragma unroll
           for (int e = 0; e < 8; e += 2)
             sum = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pf[kb][jj][qb][e], pf[kb][jj][qb][e + 1]}, ones, sum, false);
@@ -414,7 +415,9 @@ struct Variant {
 // (Measured and dropped: twelve-wave rings of 4 and 6 stages (1-2% slower than 3), eight of the
 // twelve waves fetching instead of four (2% slower), 64-key tiles at twelve waves (spills); an eight-wave ping-pong of MFMA and softmax phases, 1.8x slower at the
 // trunk shape; a software-pipelined wave issuing tile t - 1's P.V MFMAs around tile t's softmax,
-// no faster than variant 1; 64- and 96-row waves at one wave per SIMD, 1.5-1.9x slower.)
+// no faster than variant 1; a twelve-wave form issuing tile t + 1's S MFMAs between tile t's
+// softmax instructions (4-stage ring), 1% faster than variant 4; 64- and 96-row waves at one
+// wave per SIMD, 1.5-1.9x slower.)
 constexpr Variant kVariants[] = {
     {1, 2, 64, true}, {1, 2, 32, true}, {1, 2, 64, false}, {1, 3, 32, false}, {1, 3, 32, false, 12}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
