@@ -253,6 +253,12 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
         kf[slot][kb] = *reinterpret_cast<const bf16x8*>(kl + r * kHd + 8 * ((2 * st + g) ^ swz<16>(r)));
       }
     };
+    // The S MFMAs issue at a raised wave priority: a wave in its MFMA phase is picked before the
+    // waves of its SIMD that are in their softmax, which fill the gaps between its MFMAs
+    // (trunk 4-5% and pixel-stage attention 8% faster than at one priority).
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < KD; ++st) read_k(st, st);
 #pragma unroll
@@ -272,6 +278,9 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
       __builtin_amdgcn_sched_group_barrier(0x100, KB, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, KD * KB * QB, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
 
     const int kv0 = t * KVT;
     if constexpr (MASKED) {
