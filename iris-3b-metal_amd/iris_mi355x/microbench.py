@@ -5,6 +5,11 @@
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench attention 1 20 5 4352 [--variant 4]
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench copy 1
     PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench encode-text 1 200
+    PYTHONPATH=iris-3b-metal_amd python -m iris_mi355x.microbench vendor
+
+``vendor`` times the vendor libraries at the step's shapes for comparison (not the library of
+this package): torch's BF16 ``linear`` (hipBLASLt) at the five GEMM shapes of the denoise step,
+and torch's scaled-dot-product attention at the trunk attention shape (20 heads, K/V expanded).
 
 ``fused-ops`` is the bandwidth microbenchmark of the row kernels at the single-stream block
 shape [1, 4352, 2560] BF16: RMSNorm + adaLN modulate, per-head qk-RMSNorm + 2-D RoPE for Q
@@ -176,6 +181,30 @@ def encode_text(batch: int, real: int, iters: int = 10) -> dict:
     return {"op": "encode_text", "batch": batch, "tokens": cfg.text_len, "real": real, "ms": ms}
 
 
+STEP_GEMMS = [(4352, 13696, 2560, "SwiGLU w1|w3"), (4352, 6400, 2560, "q|k|v|gate"), (4352, 2560, 2560, "proj"),
+              (4352, 2560, 6848, "w2"), (4096, 16384, 2560, "pixel adaLN")]
+
+
+def vendor(iters: int = 20) -> list[dict]:
+    """hipBLASLt (torch BF16 ``linear``) at the step's GEMM shapes and torch SDPA at the trunk
+    attention shape, HIP events on the launch stream."""
+    import torch.nn.functional as F
+
+    out = []
+    for m, n, k, name in STEP_GEMMS:
+        a = torch.randn(m, k, device="cuda").to(torch.bfloat16)
+        w = (0.02 * torch.randn(n, k, device="cuda")).to(torch.bfloat16)
+        ms = _time(lambda i: F.linear(a, w), iters)
+        out.append({"op": f"torch linear ({name})", "m": m, "n": n, "k": k, "us": ms * 1e3,
+                    "TFLOP/s": 2.0 * m * n * k / (ms * 1e-3) / 1e12})
+    b, h, n, d = 1, 20, 4352, 128
+    q, k_, v = (torch.randn(b, h, n, d, device="cuda").to(torch.bfloat16) for _ in range(3))
+    ms = _time(lambda i: F.scaled_dot_product_attention(q, k_, v), iters)
+    out.append({"op": "torch scaled_dot_product_attention", "b": b, "heads": h, "n": n, "us": ms * 1e3,
+                "TFLOP/s": 4.0 * b * n * n * h * d / (ms * 1e-3) / 1e12})
+    return out
+
+
 def copy(gib: float, iters: int = 5) -> dict:
     src = torch.ones(int(gib * (1 << 28)), device="cuda", dtype=torch.float32)
     dst = torch.empty_like(src)
@@ -202,6 +231,7 @@ def main() -> None:
     p.add_argument("--variant", type=int, default=-1)
     p = sub.add_parser("copy")
     p.add_argument("gib", type=float, nargs="?", default=1.0)
+    sub.add_parser("vendor")
     p = sub.add_parser("encode-text")
     p.add_argument("batch", type=int, nargs="?", default=1)
     p.add_argument("real", type=int, nargs="?", default=200)
@@ -217,6 +247,8 @@ def main() -> None:
         out = attention(args.b, args.h, args.hkv, args.n, variant=args.variant)
     elif args.cmd == "encode-text":
         out = encode_text(args.batch, args.real)
+    elif args.cmd == "vendor":
+        out = vendor()
     else:
         out = copy(args.gib)
     print(json.dumps(out))
