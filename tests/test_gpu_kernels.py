@@ -359,7 +359,7 @@ def _attn_inputs(b, h, hkv, n, seed):
 
 
 @pytest.mark.parametrize("n", [333, 352])
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
 def test_flash_attention_variants(variant, n):
     b, h, hkv = 1, 8, 2
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 16)
@@ -375,15 +375,16 @@ def test_flash_attention_variants(variant, n):
 
 @pytest.mark.parametrize("n", [77, 4352])
 def test_flash_attention_32_key_variants_agree_bitwise(n):
-    """The variants with 32-key tiles (register-staged, 3-stage ring, twelve-wave shared ring)
-    differ only in how K/V reach LDS: the same products and sums in the same order (each
-    exponent a single-rounding fma), so the same bits; the automatic choice between them (by
-    grid size) keeps batched and single runs equal."""
+    """The variants with 32-key tiles (register-staged, 3-stage ring, twelve-wave shared ring,
+    software-pipelined 96-row waves) differ only in how K/V reach LDS and in the order the
+    instructions issue: the same products and sums in the same order (each exponent a
+    single-rounding fma), so the same bits; the automatic choice between them (by grid size)
+    keeps batched and single runs equal."""
     b, h, hkv = 1, 20, 5
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 19)
     outs = []
     try:
-        for variant in (1, 3, 4):
+        for variant in (1, 3, 4, 5):
             _lib.call("iris_flash_attn_force_variant", variant)
             out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
             K.flash_attention(qd, kd, vt, n, None, out, n_split=0)
@@ -391,7 +392,7 @@ def test_flash_attention_32_key_variants_agree_bitwise(n):
     finally:
         _lib.call("iris_flash_attn_force_variant", -1)
     for i in range(1, len(outs)):
-        assert torch.equal(outs[0], outs[i]), f"variant {(1, 3, 4)[i]} differs from variant 1"
+        assert torch.equal(outs[0], outs[i]), f"variant {(1, 3, 4, 5)[i]} differs from variant 1"
 
 
 @pytest.mark.parametrize("b,h,hkv,n", [(1, 2, 1, 52), (2, 4, 1, 200), (1, 8, 2, 130), (1, 2, 2, 300)])
@@ -403,7 +404,7 @@ def test_flash_attention_small(b, h, hkv, n):
     close_attention(out.view(b, n, -1), want)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
 def test_flash_attention_rows_do_not_depend_on_padding_rows(variant):
     """A query row's output is bit-identical whatever the padding query rows (>= n) hold: the
     lazy max raise is decided per column, not per wave."""
@@ -509,7 +510,10 @@ def test_flash_attention_masked_text_refiner(b, h, n, mask_dtype):
     assert torch.isfinite(got.float()).all()
     close_bf16(got, want, scale=1.0, floor=4e-3)
     if b > 1:  # the all-pad prompt attends only to itself: out = v, to BF16 rounding
-        torch.testing.assert_close(got[1].float().cpu(), v[1].transpose(0, 1).reshape(n, h * 128).float())
+        # (its one probability enters P.V rounded to BF16 and the normaliser unrounded, so the
+        # output is v to one BF16 step: relative 2^-7)
+        torch.testing.assert_close(got[1].float().cpu(), v[1].transpose(0, 1).reshape(n, h * 128).float(),
+                                   rtol=2.0**-7, atol=0.0)
 
 
 @pytest.mark.parametrize("seqs,L,heads,d", [(37, 12, 32, 80), (50, 3, 4, 16), (5, 16, 1, 128)])
