@@ -427,29 +427,36 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
 // accumulator at least two groups after its last MFMA, a P word is read by an MFMA at least
 // four instructions after its conversion, and the paths that touch accumulators sooner (the
 // rare max raise, the tail mask, the epilogue) start with explicit wait states.
-#define IRIS_EXP "v_fma_f32 %[x], %[s], %[k], -%[m]\n\tv_exp_f32 %[x], %[x]\n\t"
+#define IRIS_EXP "v_exp_f32 %[x], %[f]\n\t"
+#define IRIS_NEXT "v_fma_f32 %[fn], %[sn], %[k], -%[m]\n\t"
 #define IRIS_PACK "v_cvt_pk_bf16_f32 %[w], %[x0], %[x]\n\t"
 #define IRIS_ADD "v_add_f32 %[sum], %[sum], %[x]\n\t"
 
-// one S MFMA (VGPR accumulator c; ZERO: starting from zero) with one softmax step: x =
-// exp2(s * k - m) before it, added to sum after it; on odd steps also the pair (x0, x)
-// converted to a BF16 word w
-template <bool ZERO, bool ODD>
-__device__ __forceinline__ void s_step(f32x16& c, const bf16x8& a, const bf16x8& b, float s, float k, float m,
-                                       float& x, float x0, unsigned& w, float& sum) {
+// One softmax step per MFMA. Step j of a 16-key half takes f = s_j * k - m (from the step
+// before: no VALU instruction waits on the one just issued), issues x = exp2(f), the next
+// step's fma (NEXT), the MFMA, then on odd steps the pair (x0, x) converted to a BF16 word w,
+// and adds x to sum.
+// S MFMA (VGPR accumulator c; ZERO: starting from zero, step 0)
+template <bool ZERO, bool ODD, bool NEXT>
+__device__ __forceinline__ void s_step(f32x16& c, const bf16x8& a, const bf16x8& b, float f, float sn, float k,
+                                       float m, float& x, float& fn, float x0, unsigned& w, float& sum) {
+  static_assert(!ZERO || (!ODD && NEXT), "the zero-start step is step 0");
   if constexpr (ZERO) {
-    static_assert(!ODD, "the zero-start step is step 0");
-    asm volatile(IRIS_EXP "v_mfma_f32_32x32x16_bf16 %[c], %[a], %[b], 0\n\t" IRIS_ADD
-                 : [c] "=&v"(c), [x] "=&v"(x), [sum] "+v"(sum)
-                 : [a] "v"(a), [b] "v"(b), [s] "v"(s), [k] "s"(k), [m] "v"(m));
+    asm volatile(IRIS_EXP IRIS_NEXT "v_mfma_f32_32x32x16_bf16 %[c], %[a], %[b], 0\n\t" IRIS_ADD
+                 : [c] "=&v"(c), [x] "=&v"(x), [fn] "=&v"(fn), [sum] "+v"(sum)
+                 : [a] "v"(a), [b] "v"(b), [f] "v"(f), [sn] "v"(sn), [k] "s"(k), [m] "v"(m));
   } else if constexpr (!ODD) {
-    asm volatile(IRIS_EXP "v_mfma_f32_32x32x16_bf16 %[c], %[a], %[b], %[c]\n\t" IRIS_ADD
-                 : [c] "+v"(c), [x] "=&v"(x), [sum] "+v"(sum)
-                 : [a] "v"(a), [b] "v"(b), [s] "v"(s), [k] "s"(k), [m] "v"(m));
+    asm volatile(IRIS_EXP IRIS_NEXT "v_mfma_f32_32x32x16_bf16 %[c], %[a], %[b], %[c]\n\t" IRIS_ADD
+                 : [c] "+v"(c), [x] "=&v"(x), [fn] "=&v"(fn), [sum] "+v"(sum)
+                 : [a] "v"(a), [b] "v"(b), [f] "v"(f), [sn] "v"(sn), [k] "s"(k), [m] "v"(m));
+  } else if constexpr (NEXT) {
+    asm volatile(IRIS_EXP IRIS_NEXT "v_mfma_f32_32x32x16_bf16 %[c], %[a], %[b], %[c]\n\t" IRIS_PACK IRIS_ADD
+                 : [c] "+v"(c), [x] "=&v"(x), [fn] "=&v"(fn), [w] "=&v"(w), [sum] "+v"(sum)
+                 : [a] "v"(a), [b] "v"(b), [f] "v"(f), [sn] "v"(sn), [k] "s"(k), [m] "v"(m), [x0] "v"(x0));
   } else {
     asm volatile(IRIS_EXP "v_mfma_f32_32x32x16_bf16 %[c], %[a], %[b], %[c]\n\t" IRIS_PACK IRIS_ADD
                  : [c] "+v"(c), [x] "=&v"(x), [w] "=&v"(w), [sum] "+v"(sum)
-                 : [a] "v"(a), [b] "v"(b), [s] "v"(s), [k] "s"(k), [m] "v"(m), [x0] "v"(x0));
+                 : [a] "v"(a), [b] "v"(b), [f] "v"(f), [x0] "v"(x0));
   }
 }
 
@@ -491,25 +498,31 @@ __device__ __forceinline__ void s_step(f32x16& c, const bf16x8& a, const bf16x8&
 #define IRIS_CL16(...) IRIS_CL16_(__VA_ARGS__)
 
 // one P.V MFMA into accumulator tile K with one softmax step, as s_step
-template <int K, bool ODD>
-__device__ __forceinline__ void o_step(const bf16x8& a, const bf16x8& b, float s, float k, float m, float& x, float x0,
-                                       unsigned& w, float& sum) {
-#define IRIS_O_CASE(kk)                                                                                              \
-  if constexpr (K == kk) {                                                                                           \
-    if constexpr (!ODD)                                                                                              \
-      asm volatile(IRIS_EXP "v_mfma_f32_32x32x16_bf16 " IRIS_ACC_##kk ", %[a], %[b], " IRIS_ACC_##kk "\n\t" IRIS_ADD \
-                   : [x] "=&v"(x), [sum] "+v"(sum)                                                                   \
-                   : [a] "v"(a), [b] "v"(b), [s] "v"(s), [k] "s"(k), [m] "v"(m)                                      \
-                   : IRIS_CL16(IRIS_EL_##kk));                                                                       \
-    else                                                                                                             \
-      asm volatile(IRIS_EXP "v_mfma_f32_32x32x16_bf16 " IRIS_ACC_##kk ", %[a], %[b], " IRIS_ACC_##kk                 \
-                   "\n\t" IRIS_PACK IRIS_ADD                                                                          \
-                   : [x] "=&v"(x), [w] "=&v"(w), [sum] "+v"(sum)                                                     \
-                   : [a] "v"(a), [b] "v"(b), [s] "v"(s), [k] "s"(k), [m] "v"(m), [x0] "v"(x0)                        \
-                   : IRIS_CL16(IRIS_EL_##kk));                                                                       \
+template <int K, bool ODD, bool NEXT>
+__device__ __forceinline__ void o_step(const bf16x8& a, const bf16x8& b, float f, float sn, float k, float m, float& x,
+                                       float& fn, float x0, unsigned& w, float& sum) {
+#define IRIS_O_MFMA(kk) "v_mfma_f32_32x32x16_bf16 " IRIS_ACC_##kk ", %[a], %[b], " IRIS_ACC_##kk "\n\t"
+#define IRIS_O_CASE(kk)                                                                                  \
+  if constexpr (K == kk) {                                                                               \
+    if constexpr (!ODD)                                                                                  \
+      asm volatile(IRIS_EXP IRIS_NEXT IRIS_O_MFMA(kk) IRIS_ADD                                           \
+                   : [x] "=&v"(x), [fn] "=&v"(fn), [sum] "+v"(sum)                                       \
+                   : [a] "v"(a), [b] "v"(b), [f] "v"(f), [sn] "v"(sn), [k] "s"(k), [m] "v"(m)            \
+                   : IRIS_CL16(IRIS_EL_##kk));                                                           \
+    else if constexpr (NEXT)                                                                             \
+      asm volatile(IRIS_EXP IRIS_NEXT IRIS_O_MFMA(kk) IRIS_PACK IRIS_ADD                                 \
+                   : [x] "=&v"(x), [fn] "=&v"(fn), [w] "=&v"(w), [sum] "+v"(sum)                         \
+                   : [a] "v"(a), [b] "v"(b), [f] "v"(f), [sn] "v"(sn), [k] "s"(k), [m] "v"(m), [x0] "v"(x0) \
+                   : IRIS_CL16(IRIS_EL_##kk));                                                           \
+    else                                                                                                 \
+      asm volatile(IRIS_EXP IRIS_O_MFMA(kk) IRIS_PACK IRIS_ADD                                           \
+                   : [x] "=&v"(x), [w] "=&v"(w), [sum] "+v"(sum)                                         \
+                   : [a] "v"(a), [b] "v"(b), [f] "v"(f), [x0] "v"(x0)                                    \
+                   : IRIS_CL16(IRIS_EL_##kk));                                                           \
   }
   IRIS_TILES(IRIS_O_CASE)
 #undef IRIS_O_CASE
+#undef IRIS_O_MFMA
 }
 // accumulator tile K <-> VGPRs
 template <int K>
@@ -552,6 +565,7 @@ __device__ __forceinline__ void acc_zero_all() {
 #undef IRIS_Z_CASE
 }
 #undef IRIS_EXP
+#undef IRIS_NEXT
 #undef IRIS_PACK
 #undef IRIS_ADD
 
@@ -632,17 +646,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int vd = (w * LOADS + j) * VRPL + lane / VCPR;
     v_off[j] = vd * static_cast<int>(n_pad) + 8 * ((lane % VCPR) ^ swz<VCPR>(vd));
   }
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc((void*)kh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc((void*)vh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
   auto issue = [&](int t, int stage) {
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
     bf16* kl = lds + stage * STAGE;
     bf16* vl = kl + TILE;
+    // tile offsets as scalars (the compiler otherwise keeps them in VGPRs here and wraps each
+    // load in a loop over lanes)
+    const int so_k = __builtin_amdgcn_readfirstlane(t * KVT * kHd * 2);
+    const int so_v = __builtin_amdgcn_readfirstlane(t * KVT * 2);
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      buffer_load_lds16(rk, kl + (w * LOADS + j) * 512, k_off[j] * 2, t * KVT * kHd * 2);
-      buffer_load_lds16(rv, vl + (w * LOADS + j) * 512, v_off[j] * 2, t * KVT * 2);
+      buffer_load_lds16(rk, kl + (w * LOADS + j) * 512, k_off[j] * 2, so_k);
+      buffer_load_lds16(rv, vl + (w * LOADS + j) * 512, v_off[j] * 2, so_v);
     }
   };
 
@@ -653,11 +671,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const float sl2 = p.scale_log2;
   const int n_tiles = (p.n + KVT - 1) / KVT;
 
-  f32x16 sacc[4];       // S^T accumulators: tile t block x in sacc[(3 t + x) % 4]
-  unsigned pw[2][2][4];  // P^T words of tile t block x: pw[(t + x) % 2][16-key half][word]
-  constexpr int KD = 3;
+  f32x16 sacc[QB];        // S^T of block x: tile t's until its max decision, then tile t + 1's
+  unsigned pw[QB][2][4];  // P^T words of block x: [16-key half][word]
+  constexpr int KD = 4;
   bf16x8 kf[KD];
-  constexpr int VD = 4;
+  constexpr int VD = 6;
   bf16x8 vfr[VD];
   auto read_k = [&](const bf16* kl, int st, int slot) {
     kf[slot] = *reinterpret_cast<const bf16x8*>(kl + l32 * kHd + 8 * ((2 * st + g) ^ swz<16>(l32)));
@@ -666,156 +684,154 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int jj = i / 4, d = (i % 4) * 32 + l32;
     vfr[slot] = *reinterpret_cast<const bf16x8*>(vl + d * KVT + 8 * ((2 * jj + g) ^ swz<VCPR>(d)));
   };
-  auto pword = [&](int pb, int half) {
-    return __builtin_bit_cast(bf16x8, (unsigned __attribute__((ext_vector_type(4)))){pw[pb][half][0], pw[pb][half][1],
-                                                                                       pw[pb][half][2], pw[pb][half][3]});
+  auto pword = [&](int x, int half) {
+    return __builtin_bit_cast(bf16x8, (unsigned __attribute__((ext_vector_type(4)))){pw[x][half][0], pw[x][half][1],
+                                                                                       pw[x][half][2], pw[x][half][3]});
   };
 
-  // S group: tile t + 1's S^T of block y into sacc[n] (K fragments 0 .. KD - 1 already read),
-  // carrying half 1 of block x's probabilities (sacc[c] -> pw[pb][1]); reads the next P.V
-  // group's first VD V^T fragments (vl) behind its last MFMAs.
-  auto s_group = [&](auto yc, auto nc, auto cc, auto xc, auto pbc, const bf16* kl, const bf16* vl) {
-    constexpr int y = decltype(yc)::value, n = decltype(nc)::value, c = decltype(cc)::value;
-    constexpr int x = decltype(xc)::value, pb = decltype(pbc)::value;
+  // S group: tile t + 1's S^T of block y into sacc[y] (its K fragments 0 .. KD - 1 already
+  // read), carrying half 1 of block x's probabilities (sacc[x] -> pw[x][1], added to sum[x]);
+  // reads the next P.V group's first VD V^T fragments (vl) behind its last MFMAs.
+  auto s_group = [&](auto yc, auto xc, const bf16* kl, const bf16* vl) {
+    constexpr int y = decltype(yc)::value, x = decltype(xc)::value;
+    static_assert(x != y, "the softmax reads another block's scores");
     float xv[8];
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const float sv = sacc[c][8 + st];
-      if (st == 0)
-        s_step<true, false>(sacc[n], kf[0], qf[y][0], sv, sl2, m_run[x], xv[0], 0.0f, pw[pb][1][0], sum[x]);
-      else if (st % 2 == 0)
-        s_step<false, false>(sacc[n], kf[st % KD], qf[y][st], sv, sl2, m_run[x], xv[st], 0.0f, pw[pb][1][0], sum[x]);
-      else
-        s_step<false, true>(sacc[n], kf[st % KD], qf[y][st], sv, sl2, m_run[x], xv[st], xv[st - 1], pw[pb][1][st / 2],
-                           sum[x]);
-      if (st + KD < 8) read_k(kl, st + KD, st % KD);
-      if (st >= 5) read_v(vl, st - 5, st - 5);
-      if (st == 7) read_v(vl, 3, 3);
-    }
-  };
-  // P.V group: tile t's O^T += V^T P^T of block y (words pw[py]; V^T fragments 0 .. VD - 1
-  // already read), carrying half 0 of block x's probabilities (sacc[c] -> pw[pb][0], sum[x]
-  // restarted); reads the next S group's first KD K fragments (kl) behind its last MFMAs.
-  auto o_group = [&](auto yc, auto pyc, auto cc, auto xc, auto pbc, const bf16* vl, const bf16* kl) {
-    constexpr int y = decltype(yc)::value, py = decltype(pyc)::value, c = decltype(cc)::value;
-    constexpr int x = decltype(xc)::value, pb = decltype(pbc)::value;
-    const bf16x8 p0 = pword(py, 0), p1 = pword(py, 1);
-    float xv[8];
-    sum[x] = 0.0f;
-    static_for<8>([&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      const float sv = sacc[c][i];
-      if constexpr (i % 2 == 0)
-        o_step<4 * y + i % 4, false>(vfr[i % VD], i < 4 ? p0 : p1, sv, sl2, m_run[x], xv[i], 0.0f, pw[pb][0][0], sum[x]);
-      else
-        o_step<4 * y + i % 4, true>(vfr[i % VD], i < 4 ? p0 : p1, sv, sl2, m_run[x], xv[i], xv[i - 1],
-                                    pw[pb][0][i / 2], sum[x]);
-      if constexpr (i + VD < 8) read_v(vl, i + VD, i % VD);
-      if constexpr (i >= 5) read_k(kl, i - 5, i - 5);
+    float f = __builtin_fmaf(sacc[x][8], sl2, -m_run[x]);
+    static_for<8>([&](auto stc) {
+      constexpr int st = decltype(stc)::value;
+      const float sn = sacc[x][8 + (st + 1) % 8];
+      float fn;
+      s_step<st == 0, st % 2 == 1, st < 7>(sacc[y], kf[st % KD], qf[y][st], f, sn, sl2, m_run[x], xv[st], fn,
+                                           xv[(st + 7) % 8], pw[x][1][st / 2], sum[x]);
+      f = fn;
+      if constexpr (st + KD < 8) read_k(kl, st + KD, st % KD);
+      if constexpr (st >= 8 - VD) read_v(vl, st - (8 - VD), st - (8 - VD));
     });
   };
-  // recomputes one half of block qb's probabilities against m (the max raise's path)
-  auto probs_half = [&](const f32x16& s, int pb, int half, float m, float& acc) {
+  // P.V group: tile t's O^T += V^T P^T of block y (words pw[y]; V^T fragments 0 .. VD - 1
+  // already read), carrying half 0 of block x's probabilities (sacc[x] -> pw[x][0], sum[x]
+  // restarted); reads the next S group's first KD K fragments (kl) behind its last MFMAs.
+  auto o_group = [&](auto yc, auto xc, const bf16* vl, const bf16* kl) {
+    constexpr int y = decltype(yc)::value, x = decltype(xc)::value;
+    static_assert(x != y, "the words read and the words written are another block's");
+    const bf16x8 p0 = pword(y, 0), p1 = pword(y, 1);
+    float xv[8];
+    sum[x] = 0.0f;
+    float f = __builtin_fmaf(sacc[x][0], sl2, -m_run[x]);
+    static_for<8>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const float sn = sacc[x][(i + 1) % 8];
+      float fn;
+      o_step<4 * y + i % 4, i % 2 == 1, i < 7>(vfr[i % VD], i < 4 ? p0 : p1, f, sn, sl2, m_run[x], xv[i], fn,
+                                               xv[(i + 7) % 8], pw[x][0][i / 2], sum[x]);
+      f = fn;
+      if constexpr (i + VD < 8) read_v(vl, i + VD, i % VD);
+      if constexpr (i >= 8 - KD) read_k(kl, i - (8 - KD), i - (8 - KD));
+    });
+  };
+  // one half of block x's probabilities against m, written to its words and added to acc (the
+  // prologue's and the max raise's path)
+  auto probs_half = [&](int x, int half, float m, float& acc) {
     bf16x8 ph;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * half + e], sl2, -m));
-      ph[e] = from_f32<bf16>(x);
-      acc += x;
+      const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[x][8 * half + e], sl2, -m));
+      ph[e] = from_f32<bf16>(v);
+      acc += v;
     }
     const auto wv = __builtin_bit_cast(unsigned __attribute__((ext_vector_type(4))), ph);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pw[pb][half][e] = wv[e];
+    for (int e = 0; e < 4; ++e) pw[x][half][e] = wv[e];
   };
-  // the lazy max raise of flash_attn_kernel for block qb (wave-uniform decision)
-  auto settle = [&](auto qbc, auto cc, auto pbc) {
-    constexpr int qb = decltype(qbc)::value, c = decltype(cc)::value, pb = decltype(pbc)::value;
-    const int need = !(sum[qb] <= 256.0f);
-    if (__any(need)) {
+  // which lanes of block x need the max raise; the compare issues here, its result is read a
+  // group later, so the wave never waits on it
+  auto raise_mask = [&](int x) {
+    const unsigned long long m = __ballot(!(sum[x] <= 256.0f));
+    asm volatile("" ::"s"(m));
+    return m;
+  };
+  // the lazy max raise of flash_attn_kernel for block x (m: raise_mask's lanes), then the sum
+  // joins l
+  auto settle = [&](auto xc, unsigned long long mask) {
+    constexpr int x = decltype(xc)::value;
+    if (__builtin_expect(mask != 0, 0)) {  // out of line: the common path takes no branch
       mfma_drain();
+      const int need = !(sum[x] <= 256.0f);
       const int partner = __shfl_xor(need, 32);
       const bool up = need || partner;
       float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[x][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = up ? fmaxf(m_run[qb], mx * sl2) : m_run[qb];
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-      l_run[qb] *= alpha;
+      const float m_new = up ? fmaxf(m_run[x], mx * sl2) : m_run[x];
+      const float alpha = __builtin_amdgcn_exp2f(m_run[x] - m_new);
+      l_run[x] *= alpha;
       static_for<4>([&](auto dbc) {
-        constexpr int k = 4 * qb + decltype(dbc)::value;
+        constexpr int k = 4 * x + decltype(dbc)::value;
         acc_write<k>(acc_read<k>() * alpha);
       });
-      m_run[qb] = m_new;
+      m_run[x] = m_new;
       float sm = 0.0f;
-      probs_half(sacc[c], pb, 0, m_new, sm);
-      probs_half(sacc[c], pb, 1, m_new, sm);
-      sum[qb] = sm;
-      mfma_drain(pw[pb]);  // the P.V MFMAs next read these words
+      probs_half(x, 0, m_new, sm);
+      probs_half(x, 1, m_new, sm);
+      sum[x] = sm;
+      mfma_drain(pw[x]);  // the P.V MFMAs read these words next
     }
-    l_run[qb] += sum[qb];
+    l_run[x] += sum[x];
   };
-  auto mask_tail = [&](f32x16& s, int kv0) {
+  // keys >= n of tile t do not exist (its scores in sacc[x], just out of the MFMAs)
+  auto mask_tail = [&](int x, int t) {
+    mfma_drain(sacc[0], sacc[1], sacc[2]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int key = kv0 + 8 * (r >> 2) + 4 * g + (r & 3);
-      if (key >= p.n) s[r] = -INFINITY;
+      const int key = t * KVT + 8 * (r >> 2) + 4 * g + (r & 3);
+      if (key >= p.n) sacc[x][r] = -INFINITY;
     }
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
 
-  // tile t (U = t % 4): S(t+1)[0] | P.V(t)[0] | S(t+1)[1] | P.V(t)[1] | S(t+1)[2] | barrier | P.V(t)[2]
-  auto tile = [&](int t, auto uc) {
-    constexpr int U = decltype(uc)::value;
-    using C0 = std::integral_constant<int, (3 * U) % 4>;
-    using C1 = std::integral_constant<int, (3 * U + 1) % 4>;
-    using C2 = std::integral_constant<int, (3 * U + 2) % 4>;
-    using N0 = std::integral_constant<int, (3 * U + 3) % 4>;
-    using N1 = std::integral_constant<int, (3 * U + 4) % 4>;
-    using N2 = std::integral_constant<int, (3 * U + 5) % 4>;
-    using P0 = std::integral_constant<int, U % 2>;        // (t + 0) % 2
-    using P1 = std::integral_constant<int, (U + 1) % 2>;  // (t + 1) % 2: block 1 of tile t, block 0 of t + 1
+  // tile t: S(t+1)[0] | P.V(t)[0] | S(t+1)[1] | P.V(t)[1] | S(t+1)[2] | barrier | P.V(t)[2]; each
+  // group carries one half of a block's softmax, and block x's max decision comes one group
+  // after its sums are complete, before its P.V. TAIL: tile t + 1 is the last tile (masked when
+  // partial); LAST: tile t is (the products of tile t + 1 are never used).
+  auto tile = [&](int t, auto tailc, auto lastc) {
+    constexpr bool TAIL = decltype(tailc)::value, LAST = decltype(lastc)::value;
     const bf16* kl = lds + ((t + 1) % STAGES) * STAGE;
     const bf16* vl = lds + (t % STAGES) * STAGE + TILE;
     const bf16* kl2 = lds + ((t + 2) % STAGES) * STAGE;
+    const bool partial = TAIL && (t + 2) * KVT > p.n;
 
-    s_group(I0{}, N0{}, C0{}, I0{}, P0{}, kl, vl);
-    settle(I0{}, C0{}, P0{});
-    o_group(I0{}, P0{}, C1{}, I1{}, P1{}, vl, kl);
-    s_group(I1{}, N1{}, C1{}, I1{}, P1{}, kl, vl);
-    settle(I1{}, C1{}, P1{});
-    o_group(I1{}, P1{}, C2{}, I2{}, P0{}, vl, kl);
-    s_group(I2{}, N2{}, C2{}, I2{}, P0{}, kl, vl);
-    settle(I2{}, C2{}, P0{});
-    if ((t + 2) * KVT > p.n && t + 1 < n_tiles) {  // tile t + 1 is the tail tile: keys >= n do not exist
-      mfma_drain(sacc[N0::value], sacc[N1::value], sacc[N2::value]);
-      mask_tail(sacc[N0::value], (t + 1) * KVT);
-      mask_tail(sacc[N1::value], (t + 1) * KVT);
-      mask_tail(sacc[N2::value], (t + 1) * KVT);
-    }
+    s_group(I0{}, I1{}, kl, vl);
+    const unsigned long long r1 = raise_mask(1);
+    if (partial) mask_tail(0, t + 1);
+    o_group(I0{}, I2{}, vl, kl);
+    settle(I1{}, r1);
+    s_group(I1{}, I2{}, kl, vl);
+    const unsigned long long r2 = raise_mask(2);
+    if (partial) mask_tail(1, t + 1);
+    o_group(I1{}, I0{}, vl, kl);
+    settle(I2{}, r2);
+    s_group(I2{}, I0{}, kl, vl);
+    const unsigned long long r0 = raise_mask(0);
+    if (partial) mask_tail(2, t + 1);
     // tile t + 2 visible for the next tile's first group (tiles up to t + STAGES - 2 were
-    // issued); stage (t - 1) % STAGES no longer read: refilled with tile t + STAGES - 1
-    if (t + STAGES - 2 < n_tiles)
-      wait_vmcnt<(STAGES - 4) * LPW>();
-    else
-      wait_vmcnt<0>();
+    // issued); stage (t - 1) % STAGES no longer read: refilled with tile t + STAGES - 1 (past the
+    // end the last tile again, into a stage nothing reads, so every tile waits and loads alike)
+    wait_vmcnt<(STAGES - 4) * LPW>();
     __builtin_amdgcn_s_barrier();
-    if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
-    o_group(I2{}, P0{}, N0{}, I0{}, P1{}, vl, kl2);
+    issue(min(t + STAGES - 1, n_tiles - 1), (t + STAGES - 1) % STAGES);
+    o_group(I2{}, I1{}, vl, kl2);
+    if constexpr (!LAST) settle(I0{}, r0);
   };
 
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < n_tiles) issue(s, s);
-  if (STAGES - 2 < n_tiles)  // tiles 0 and 1 landed
-    wait_vmcnt<(STAGES - 3) * LPW>();
-  else
-    wait_vmcnt<0>();
+  for (int s = 0; s < STAGES - 1; ++s) issue(min(s, n_tiles - 1), s);
+  wait_vmcnt<(STAGES - 3) * LPW>();  // tiles 0 and 1 landed
   __builtin_amdgcn_s_barrier();
-  // tile 0's S^T, block 0's first half, the first fragments of the first two groups
+  // tile 0's S^T; block 0's probabilities and max decision, block 1's first half; the first K
+  // fragments of the first group
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
@@ -830,28 +846,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   mfma_drain(sacc[0], sacc[1], sacc[2]);
   if (KVT > p.n) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) mask_tail(sacc[qb], 0);
+    for (int qb = 0; qb < QB; ++qb) mask_tail(qb, 0);
   }
-  {
-    float sm = 0.0f;
-    probs_half(sacc[0], 0, 0, m_run[0], sm);
-    sum[0] = sm;
-  }
+  probs_half(0, 0, m_run[0], sum[0]);
+  probs_half(0, 1, m_run[0], sum[0]);
+  settle(I0{}, raise_mask(0));
+  probs_half(1, 0, m_run[1], sum[1]);
 #pragma unroll
   for (int st = 0; st < KD; ++st) read_k(lds + STAGE, st, st);
-  using U0 = std::integral_constant<int, 0>;
-  using U1 = std::integral_constant<int, 1>;
-  using U2 = std::integral_constant<int, 2>;
-  using U3 = std::integral_constant<int, 3>;
-  for (int t = 0; t < n_tiles; t += 4) {
-    tile(t, U0{});
-    if (t + 1 >= n_tiles) break;
-    tile(t + 1, U1{});
-    if (t + 2 >= n_tiles) break;
-    tile(t + 2, U2{});
-    if (t + 3 >= n_tiles) break;
-    tile(t + 3, U3{});
-  }
+  using F = std::false_type;
+  using T = std::true_type;
+  int t = 0;
+  for (; t + 2 < n_tiles; ++t) tile(t, F{}, F{});
+  if (t + 1 < n_tiles) tile(t++, T{}, F{});
+  tile(t, F{}, T{});
+  wait_vmcnt<0>();  // the repeated loads past the last tile land before the workgroup ends
   mfma_drain();
 
   static_for<QB>([&](auto qbc) {
