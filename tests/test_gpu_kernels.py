@@ -309,6 +309,47 @@ def test_gemm_bf16_output_over_several_rounds(tile, shape, swiglu):
     close_bf16(out[rows], want)
 
 
+@pytest.mark.parametrize("nk,bias", [((2560, 6848), False), ((16384, 2560), True), ((1280, 4096), True),
+                                     ((3840, 1280), False), ((1280, 1280), True), ((4096, 1280), True)])
+def test_gemm_hipblaslt_shapes_eager_and_graph_replays(nk, bias):
+    """The plain GEMMs routed to hipBLASLt (BF16 output, optional FP32 bias): against an FP32
+    product on sampled rows, the same as the library's own four-wave kernel to BF16 rounding,
+    and bit for bit the same when recorded in a HIP graph and replayed several times with eager
+    work and synchronisation between the replays."""
+    n, k = nk
+    m = 4352 if n == 2560 else 4096
+    g = torch.Generator(device=DEV).manual_seed(41)
+    a = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16)
+    b = torch.randn(n, generator=g, device=DEV) if bias else None
+    eager = K.linear(a, w, b)
+    _lib.call("iris_gemm_force_tile", 11 if n >= 2560 else 12)
+    try:
+        own = K.linear(a, w, b)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    rows = torch.cat([torch.arange(0, m, 53), torch.tensor([m - 1])])
+    want = _gemm_ref(a[rows], w, b)
+    close_bf16(eager[rows], want)
+    close_bf16(eager[rows], own[rows].float())
+    out = torch.empty_like(eager)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        K.linear(a, w, b, out=out)  # the problem's set-up happens outside the capture
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        K.linear(a, w, b, out=out)
+    for _ in range(4):
+        out.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        K.linear(a[:64], w, b)  # eager work between the replays
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("shape", [(4352, 6400, 2560), (4096, 16384, 2560)])
 def test_gemm_trunk_shapes(shape):
     m, n, k = shape
