@@ -392,7 +392,7 @@ def main() -> None:
     roofline = {"bound": "mfma", "kernel": "gemm_w4_kernel<256, SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
                 **rate(True), "traffic": profiled_traffic(),
                 "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
-    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel, gemm_kernel)", **rate(False)}
+    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel, gemm_kernel, hipBLASLt for the plain shapes)", **rate(False)}
     attention = {"kernel": "flash_attn_kernel, trunk joint attention (20 query / 5 K/V heads)",
                  **timer.attention_summary(cfg.num_heads)}
     attention_pixel = {"kernel": "flash_attn_kernel, pixel-stage attention (10 heads)",
