@@ -305,7 +305,7 @@ def main() -> None:
     ap.add_argument("--no-extras", action="store_true", help="skip the fused-op, single-block and guided legs")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported",
+        print(json.dumps({"error": "this benchmark runs on one GPU; --gpus above 1 is not supported",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 

@@ -1,6 +1,6 @@
 """FP32 CPU oracle of the Iris-3B denoiser forward, its text adapter and samplers.
 
-TEST INFRASTRUCTURE ONLY. This module is the checker that the HIP path is
+TEST INFRASTRUCTURE ONLY. This module is the reference the HIP path is
 compared against. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import it; the product package never
 does, and it is never a fallback for the GPU path.

@@ -1,4 +1,4 @@
-"""The north-star parity bar shared by the end-to-end GPU tests.
+"""The end-to-end parity bar shared by the GPU forward tests.
 
 Predicted flow against the FP32 oracle: cosine similarity >= 0.999 and max relative error
 (max |got - want| / max |want|) <= 2e-2. Both are evaluated in float64: in FP32 the cosine

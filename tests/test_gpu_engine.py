@@ -1,6 +1,6 @@
 """End-to-end parity of the HIP forward against the FP32 CPU oracle.
 
-Bar (from the north-star spec, ``tests/parity.py``): predicted-flow cosine >= 0.999 and max
+Bar (``tests/parity.py``): predicted-flow cosine >= 0.999 and max
 relative error (max |got - want| / max |want|) <= 2e-2, BF16 MFMA path versus FP32 reference."""
 
 import pytest
@@ -200,7 +200,7 @@ def _all_cores():
 def test_iris3b_full_depth_forward_at_1024_matches_oracle(iris3b_full, iris3b_full_weights):
     """The benchmarked workload itself: full-depth Iris-3B at 1024x1024, batch 1, 256 N(0,1)
     prepared text tokens, model time 500, against the FP32 oracle forward (the reference's
-    engine-vs-upstream check, tests/test_metal_engine.py:73-91, at the north-star bar)."""
+    engine-vs-upstream check, tests/test_metal_engine.py:73-91, at the end-to-end bar)."""
     _, sd = iris3b_full_weights
     g = torch.Generator().manual_seed(0)
     x = torch.randn(1, 3, 1024, 1024, generator=g)
