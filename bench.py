@@ -8,7 +8,7 @@ N(0, 1) prepared text tokens (the text adapter is outside the step, as in the re
 (recorded during the warm-up steps), the Euler update launched after it.
 
 Prints one JSON line. Besides the driver's fields it carries:
-- ``roofline``: the dominant kernel, the trunk's SwiGLU w1/w3 GEMM (``gemm_kernel`` with the
+- ``roofline``: the dominant kernel, the trunk's SwiGLU w1/w3 GEMM (``gemm_w4_kernel`` with the
   SwiGLU epilogue, M x 2*6826 x 2560 per block), from a second timed pass of the same steps
   launched eagerly so that every GEMM launch can be bracketed by HIP events on its stream
   (``eager_ms_per_step``): ``achieved`` = algorithmic 2*M*N*K (unpadded) over the launches'
@@ -16,7 +16,8 @@ Prints one JSON line. Besides the driver's fields it carries:
   that kernel from the committed counter summary
   ``profiles/gemm_swiglu_4352x13696x2560_traffic.txt`` (null when it is absent);
   ``gemm_all`` the same figures over every GEMM launch of the step, ``attention`` and
-  ``attention_pixel`` over the trunk's and the pixel stage's attention launches (4*N^2*H*128);
+  ``attention_pixel`` over the trunk's and the pixel stage's attention launches (4*N^2*H*128),
+  each with its HBM bytes per launch from ``profiles/attention_traffic_4352_4096.md``;
 - ``cpu_baseline``: the FP32 CPU oracle timed on this host on one full forward of the same
   workload plus its Euler update (``--cpu-turbo``: a whole 4-step Turbo sample instead);
 - ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included),
@@ -165,15 +166,16 @@ class LaunchTimer:
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_swiglu_4352x13696x2560_traffic.txt"
+ATTENTION_TRAFFIC_PROFILE = ROOT / "profiles" / "attention_traffic_4352_4096.md"
 
 
-def profiled_traffic(path: Path = TRAFFIC_PROFILE) -> float | None:
-    """HBM bytes per launch recorded by a counter summary (its ``traffic_bytes_per_launch:``
-    line), or None without one."""
+def profiled_traffic(path: Path = TRAFFIC_PROFILE, key: str = "traffic_bytes_per_launch") -> float | None:
+    """HBM bytes per launch recorded by a counter summary (its ``<key>:`` line), or None
+    without one."""
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
-        if line.strip().startswith("traffic_bytes_per_launch:"):
+        if line.strip().startswith(key + ":"):
             return float(line.split(":", 1)[1].strip().strip("`"))
     return None
 
@@ -393,10 +395,15 @@ def main() -> None:
                 **rate(True), "traffic": profiled_traffic(),
                 "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
     gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel, gemm_kernel, hipBLASLt for the plain shapes)", **rate(False)}
+    att_source = ATTENTION_TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if ATTENTION_TRAFFIC_PROFILE.exists() else None
     attention = {"kernel": "flash_attn_kernel, trunk joint attention (20 query / 5 K/V heads)",
-                 **timer.attention_summary(cfg.num_heads)}
+                 **timer.attention_summary(cfg.num_heads),
+                 "traffic": profiled_traffic(ATTENTION_TRAFFIC_PROFILE, "traffic_bytes_per_launch_trunk"),
+                 "traffic_source": att_source}
     attention_pixel = {"kernel": "flash_attn_kernel, pixel-stage attention (10 heads)",
-                       **timer.attention_summary(cfg.pixel.num_heads)}
+                       **timer.attention_summary(cfg.pixel.num_heads),
+                       "traffic": profiled_traffic(ATTENTION_TRAFFIC_PROFILE, "traffic_bytes_per_launch_pixel"),
+                       "traffic_source": att_source}
 
     turbo_s = None
     if not args.no_turbo:
