@@ -17,7 +17,7 @@ Prints one JSON line. Besides the driver's fields it carries:
   ``profiles/gemm_swiglu_4352x13696x2560_traffic.txt`` (null when it is absent);
   ``gemm_all`` the same figures over every GEMM launch of the step, ``attention`` and
   ``attention_pixel`` over the trunk's and the pixel stage's attention launches (4*N^2*H*128),
-  each with its HBM bytes per launch from ``profiles/attention_traffic_4352_4096.md``;
+  each with its HBM bytes per launch from ``profiles/attention_traffic_4352_4096.txt``;
 - ``cpu_baseline``: the FP32 CPU oracle timed on this host on one full forward of the same
   workload plus its Euler update (``--cpu-turbo``: a whole 4-step Turbo sample instead);
 - ``turbo_4step_s``: wall seconds of a whole 4-step Turbo sample (finiteness check included),
@@ -166,7 +166,7 @@ class LaunchTimer:
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_swiglu_4352x13696x2560_traffic.txt"
-ATTENTION_TRAFFIC_PROFILE = ROOT / "profiles" / "attention_traffic_4352_4096.md"
+ATTENTION_TRAFFIC_PROFILE = ROOT / "profiles" / "attention_traffic_4352_4096.txt"
 
 
 def profiled_traffic(path: Path = TRAFFIC_PROFILE, key: str = "traffic_bytes_per_launch") -> float | None:
