@@ -168,9 +168,10 @@ int iris_layer_pool(const float* h, const void* branch, const float* weight, con
  * m * lda and n * ldb below 2^30 elements (2 GiB), else IRIS_E_INVALID before any launch.
  * Plain products (IRIS_EPI_NONE, BF16 output) of the weight shapes n x k = 2560 x 6848,
  * 16384 x 2560, 1280 x 4096, 3840 x 1280, 1280 x 1280 and 4096 x 1280 at 2048 rows or more run
- * on hipBLASLt (measured faster in the denoise step); the first call of such a problem on a
- * device creates a handle, a 64 MiB workspace and the problem's plan, so it must not be made
- * while the stream is being captured into a graph (it then runs this library's kernel instead).
+ * on hipBLASLt (measured faster in the denoise step, algorithms that take no workspace); the
+ * first call of such a problem on a device creates a hipBLASLt handle and the problem's plan, so
+ * it must not be made while the stream is being captured into a graph (it then runs this
+ * library's kernel instead).
  * Its rounding order follows the row count: call one batch item at a time where rows must not
  * depend on the batch. */
 int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n, int k,

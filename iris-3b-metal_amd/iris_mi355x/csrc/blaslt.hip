@@ -5,10 +5,12 @@
 // (1280 x 1280) and expand (4096 x 1280) projections, 4096-4352 rows each. The fused GEMMs
 // (SwiGLU, q|k|v|gate, the grouped dual-stream launches, SiLU) stay on gemm.hip's kernels.
 //
-// Per device: one handle and one 64 MiB workspace, created on the first call; per problem
-// (m, n, k, strides, bias or not) a matmul descriptor, layouts and the heuristic's first
-// algorithm, cached. Set-up needs allocations and kernel-object loading, so a problem first met
-// while its stream is being captured into a graph is declined (the caller's own kernel runs); the
+// Per device: one handle, created on the first call; per problem (m, n, k, strides, bias or
+// not) a matmul descriptor, layouts and the heuristic's first algorithm among those that take
+// no workspace, cached (for these shapes the heuristic's first choice takes none at any
+// workspace cap, so the launches use no device memory beyond their operands). Set-up (the
+// handle, a problem's plan and its kernel objects) may allocate, so a problem first met while
+// its stream is being captured into a graph is declined (the caller's own kernel runs); the
 // engine runs every forward once eagerly before recording it, so the recorded graph holds the
 // hipBLASLt launches.
 #include "blaslt.hpp"
@@ -22,8 +24,6 @@
 namespace iris {
 namespace {
 
-constexpr size_t kWorkspaceBytes = size_t{64} << 20;
-
 struct Plan {
   bool ok = false;
   hipblasLtMatmulDesc_t desc = nullptr;
@@ -36,7 +36,6 @@ using Key = std::tuple<int, int, int, long, long, long, bool>;  // m, n, k, lda,
 struct DeviceState {
   bool tried = false;
   hipblasLtHandle_t handle = nullptr;
-  void* workspace = nullptr;
   std::map<Key, Plan> plans;
 };
 
@@ -65,12 +64,12 @@ Plan make_plan(hipblasLtHandle_t handle, int m, int n, int k, long lda, long ldb
   good = good && ok(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, k, m, lda));
   good = good && ok(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, n, m, ldc));
   good = good && ok(hipblasLtMatmulPreferenceCreate(&pref));
-  const uint64_t ws = kWorkspaceBytes;
+  const uint64_t ws = 0;  // algorithms without a workspace only
   good = good && ok(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)));
   hipblasLtMatmulHeuristicResult_t result{};
   int found = 0;
   good = good && ok(hipblasLtMatmulAlgoGetHeuristic(handle, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, &result, &found));
-  good = good && found > 0 && result.workspaceSize <= kWorkspaceBytes;
+  good = good && found > 0 && result.workspaceSize == 0;
   if (pref) hipblasLtMatmulPreferenceDestroy(pref);
   if (good) {
     p.algo = result.algo;
@@ -104,9 +103,8 @@ bool blaslt_linear(const bf16* a, const bf16* w, const float* bias, bf16* c, int
     if (!st.tried) {
       st.tried = true;
       if (!ok(hipblasLtCreate(&st.handle))) st.handle = nullptr;
-      if (st.handle && hipMalloc(&st.workspace, kWorkspaceBytes) != hipSuccess) st.workspace = nullptr;
     }
-    if (!st.handle || !st.workspace) return false;
+    if (!st.handle) return false;
     it = st.plans.emplace(key, make_plan(st.handle, m, n, k, lda, ldb, ldc, bias != nullptr)).first;
   }
   Plan& p = it->second;
@@ -114,8 +112,8 @@ bool blaslt_linear(const bf16* a, const bf16* w, const float* bias, bf16* c, int
   if (bias && !ok(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias))))
     return false;
   const float alpha = 1.0f, beta = 0.0f;
-  return ok(hipblasLtMatmul(st.handle, p.desc, &alpha, w, p.la, a, p.lb, &beta, c, p.lc, c, p.lc, &p.algo,
-                            st.workspace, kWorkspaceBytes, stream));
+  return ok(hipblasLtMatmul(st.handle, p.desc, &alpha, w, p.la, a, p.lb, &beta, c, p.lc, c, p.lc, &p.algo, nullptr, 0,
+                            stream));
 }
 
 }  // namespace iris
