@@ -147,19 +147,21 @@ def iris3b_blocks():
     return cfg, {k: v.cpu() for k, v in sd.items()}
 
 
-def test_iris3b_shallow_forward_at_256px_matches_oracle(iris3b_blocks):
+@pytest.mark.parametrize("batch,hw,n_text", [(1, (256, 256), 256), (2, (192, 320), 77)])
+def test_iris3b_shallow_forward_at_256px_matches_oracle(iris3b_blocks, batch, hw, n_text):
     """Full-width Iris-3B (D=2560, 20/5 heads, SwiGLU 6826, PiT 1280/10) with 1 dual + 1 single
-    + 1 pixel block, 256x256 input, 256 text tokens."""
+    + 1 pixel block: 256x256 input with 256 text tokens, and a batch of two non-square 192x320
+    inputs with 77 text tokens (joint sequences of 317 tokens, not a multiple of any tile)."""
     cfg, sd = iris3b_blocks
-    g = torch.Generator().manual_seed(3)
-    x = torch.randn(1, 3, 256, 256, generator=g)
-    t = torch.tensor([500.0])
-    text = torch.randn(1, 256, cfg.hidden_size, generator=g)
+    g = torch.Generator().manual_seed(3 + batch)
+    x = torch.randn(batch, 3, *hw, generator=g)
+    t = torch.tensor([500.0, 140.0][:batch])
+    text = torch.randn(batch, n_text, cfg.hidden_size, generator=g)
     torch.set_num_threads(max(1, torch.get_num_threads()))
     want = O.forward(sd, cfg, x, t, prepared_text=text)
     engine = HipIris(cfg, sd, device=DEV)
     got = engine(x.to(DEV), t.to(DEV), text.to(DEV))
-    check(got, want, "iris3b shallow 256px")
+    check(got, want, f"iris3b shallow B={batch} {hw} T={n_text}")
 
 
 def test_iris3b_encode_text_matches_oracle(iris3b_blocks):
