@@ -135,6 +135,18 @@ class LaunchTimer:
             fl = sum(timer.flops(x.numel() // x.shape[-1], w.shape[0], x.shape[-1], swiglu) for x, w in zip(xs, weights))
             timer.records.append((s, e, fl, swiglu))
 
+        orig_qk = K.linear_qk_rope
+
+        def linear_qk_rope(xs, weights, outs, *args, **kwargs):
+            if not timer.enabled:
+                return orig_qk(xs, weights, outs, *args, **kwargs)
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            orig_qk(xs, weights, outs, *args, **kwargs)
+            e.record()
+            fl = sum(timer.flops(x.numel() // x.shape[-1], w.shape[0], x.shape[-1], False) for x, w in zip(xs, weights))
+            timer.records.append((s, e, fl, False))
+
         orig_attn = K.flash_attention
 
         def flash_attention(q, k, vt, n, out0, out1, *args, **kwargs):
@@ -147,6 +159,7 @@ class LaunchTimer:
             timer.attention.append((s, e, 4.0 * q.shape[0] * q.shape[1] * n * n * q.shape[3], q.shape[1]))
 
         K.linear, K.linear_grouped, K.flash_attention = linear, linear_grouped, flash_attention
+        K.linear_qk_rope = linear_qk_rope
 
     def summary(self, swiglu_only: bool = False) -> tuple[float, float, int]:
         rows = [r for r in self.records if r[3] or not swiglu_only]
@@ -394,7 +407,7 @@ def main() -> None:
     roofline = {"bound": "mfma", "kernel": "gemm_w4_kernel<256, SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
                 **rate(True), "traffic": profiled_traffic(),
                 "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
-    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel, gemm_kernel, hipBLASLt for the plain shapes)", **rate(False)}
+    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel incl. the q|k|v store with Q/K norm + RoPE, gemm_kernel, hipBLASLt for the plain shapes)", **rate(False)}
     att_source = ATTENTION_TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if ATTENTION_TRAFFIC_PROFILE.exists() else None
     attention = {"kernel": "flash_attn_kernel, trunk joint attention (20 query / 5 K/V heads)",
                  **timer.attention_summary(cfg.num_heads),

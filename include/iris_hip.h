@@ -193,6 +193,25 @@ int iris_gemm_bf16_grouped(int groups, const void* const* a, const void* const* 
                            void* const* c, const int* m, int c_dtype, int n, int k, long lda, long ldb, long ldc,
                            int epilogue, hipStream_t stream);
 
+/* The q | k | v projection of an attention block with the per-head RMSNorm + RoPE of its Q and K
+ * heads done in the GEMM's store (the reference runs F.linear, then qk_norm_rope on Q and on K,
+ * src/iris_metal/model.py:236-250; src/iris_metal/kernels.py:37-84): up to two groups of equal n,
+ * k and strides as for iris_gemm_bf16_grouped, no bias. Output columns [0, 128 heads) are the Q
+ * heads and the next 128 kv_heads the K heads: they are written as iris_qk_norm_rope writes them
+ * (same results) to q BF16 [batch, heads, n_dst, 128] and k_out BF16 [batch, kv_heads, n_dst, 128],
+ * row m of group g being token t = m % rows_per_batch[g] of batch item m / rows_per_batch[g], at
+ * row dst_offset[g] + t with gains q_weight[g] / k_weight[g] and (cos, sin)[dst_offset[g] + t]
+ * (FP32 [table_rows, 64]). The remaining columns (the V heads) go to c (BF16, row stride ldc), whose
+ * Q and K columns are not written; or, with vt non-null, transposed to vt as iris_v_heads_t writes
+ * them (BF16 [batch, kv_heads, 128, n_vt], n_vt % 64 == 0; same results), which needs every group's
+ * rows_per_batch % 256 == 0 and dst_offset % 16 == 0, and then c is not written at all.
+ * n % 128 == 0; operands below 2 GiB as for iris_gemm_bf16. */
+int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const void* const* b, void* const* c, const int* m,
+                           int n, int k, long lda, long ldb, long ldc, const float* const* q_weight,
+                           const float* const* k_weight, const int* rows_per_batch, const int* dst_offset,
+                           const float* cos_table, const float* sin_table, long table_rows, void* q, void* k_out,
+                           int heads, int kv_heads, long n_dst, void* vt, long n_vt, float eps, hipStream_t stream);
+
 /* Matrix-vector products for the timestep MLP and the shared adaLN cores
  * (src/iris_metal/model.py:190-192; src/iris3b/nn/modulation.py:258-285):
  * y[b, n] = act_out(sum_k W[n, k] act_in(x[b, k]) + bias[n]), W BF16 [n, k];

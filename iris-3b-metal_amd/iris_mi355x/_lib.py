@@ -45,6 +45,8 @@ _SIGNATURES: dict[str, list] = {
     "iris_layer_pool": [P, P, P, P, c_long, c_int, c_int, P, c_int, P],
     "iris_residual_rms_norm": [P, P, c_int, P, P, c_long, c_long, c_int, c_float, P, c_int, P],
     "iris_gemm_bf16_grouped": [c_int, P, P, P, P, P, c_int, c_int, c_int, c_long, c_long, c_long, c_int, P],
+    "iris_gemm_bf16_qk_rope": [c_int, P, P, P, P, c_int, c_int, c_long, c_long, c_long, P, P, P, P, P, P, c_long,
+                               P, P, c_int, c_int, c_long, P, c_long, c_float, P],
     "iris_gemv_bf16": [P, P, c_int, c_int, c_int, P, P, c_int, P, c_int, c_int, P],
     "iris_timestep_features": [P, P, c_int, c_int, P, P],
     "iris_patchify_embed": [P, c_int, c_int, c_int, c_int, c_int, P, c_long, P, P, P, P, P, c_float, P, c_int, P,

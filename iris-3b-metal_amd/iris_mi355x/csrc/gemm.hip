@@ -35,12 +35,34 @@ struct GemmGroup {
   int tile_begin;
 };
 
+// The q | k | v projection's store with the attention inputs' per-head RMSNorm + RoPE
+// (kEpiQkRope): output columns [0, 128 heads) are the Q heads, the next 128 kv_heads the K heads,
+// written normed and rotated to q [B, heads, n_dst, 128] and k [B, kv_heads, n_dst, 128] at
+// position dst_offset + token (row m of group g is token m % rows_per_batch[g] of batch item
+// m / rows_per_batch[g]); the columns after them (the V heads) go to C unchanged.
+struct QkRope {
+  bf16 *q, *k;
+  const float *cos, *sin;  // [positions, 64]
+  const float *q_weight0, *q_weight1, *k_weight0, *k_weight1;  // per group, 128 gains each
+  int rows_per_batch0, rows_per_batch1, dst_offset0, dst_offset1;
+  int n_dst, heads, kv_heads;
+  float eps;
+  // with vt: the V heads go transposed to vt [B, kv_heads, 128, n_vt] (the layout of
+  // v_heads_t) instead of to C; needs every group's rows_per_batch % 256 == 0 and
+  // dst_offset % 16 == 0, so that a tile's 256 rows are whole 16-position groups of one item
+  bf16* vt;
+  int n_vt;
+};
+
+constexpr int kEpiQkRope = 3;  // internal epilogue code, next to the public IRIS_EPI_* values
+
 struct GemmArgs {
   GemmGroup g0, g1;
   int ngroups;
   int n, k;
   long lda, ldb, ldc;
   int total_tiles;
+  QkRope qk;  // kEpiQkRope only
 };
 
 template <typename TC>
@@ -82,6 +104,7 @@ struct TileJob {
   const float* bias;
   void* c;
   int m, tm, tn;
+  int group;
 };
 
 template <int BM, int BN>
@@ -94,7 +117,7 @@ __device__ __forceinline__ TileJob locate_tile_at(const GemmArgs& p, int tile) {
   const int group = tile / (GM * tiles_n);
   const int gm = min(GM, gr.tiles_m - group * GM);
   const int in_group = tile - group * GM * tiles_n;
-  return TileJob{gr.a, gr.b, gr.bias, gr.c, gr.m, group * GM + in_group % gm, in_group / gm};
+  return TileJob{gr.a, gr.b, gr.bias, gr.c, gr.m, group * GM + in_group % gm, in_group / gm, second ? 1 : 0};
 }
 
 template <int BM, int BN>
@@ -118,7 +141,7 @@ __device__ __forceinline__ int persistent_tile(const GemmArgs& p, int round) {
 // the end for FP32 output); the persistent kernel issues its next loads there.
 template <int BM, int BN, int WM, int WN, int FM, int FN, int NW, int RING, int EPI, typename TC, typename Mid>
 __device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, const TileJob& job, int N, long ldc,
-                                           int wm, int wn, Mid&& mid) {
+                                           int wm, int wn, const QkRope& qk, Mid&& mid) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int l32 = lane & 31;
@@ -139,6 +162,25 @@ __device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, con
     static_assert(BM * OUT_N <= RING, "output tile must fit in the LDS ring");
     bf16* cl = lds;
     __syncthreads();
+    // kEpiQkRope: the Q and K gains of this tile's group go to LDS, and thread r's rotary table row
+    // (tile row r) to registers, while the accumulators are staged
+    __shared__ float qk_gain[EPI == kEpiQkRope ? 256 : 1];
+    [[maybe_unused]] f32x4 qk_cos[EPI == kEpiQkRope ? 16 : 1], qk_sin[EPI == kEpiQkRope ? 16 : 1];
+    if constexpr (EPI == kEpiQkRope) {
+      static_assert(BM == 64 * NW, "one tile row per thread");
+      const float* __restrict__ gains = tid < 32 ? (job.group ? qk.q_weight1 : qk.q_weight0)
+                                                 : (job.group ? qk.k_weight1 : qk.k_weight0);
+      if (tid < 64) store4(qk_gain + 4 * tid, load4(gains + 4 * (tid & 31)));
+      const int rpb = job.group ? qk.rows_per_batch1 : qk.rows_per_batch0;
+      const int mm = min(tm * BM + tid, M - 1);  // (rows past M read a valid row, unused)
+      const int b = mm / rpb;
+      const long pos = (job.group ? qk.dst_offset1 : qk.dst_offset0) + (mm - b * rpb);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        qk_cos[i] = load4(qk.cos + pos * 64 + 4 * i);
+        qk_sin[i] = load4(qk.sin + pos * 64 + 4 * i);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int r = wm * WM + j * 32 + l32;
@@ -183,6 +225,99 @@ __device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, con
     constexpr int CHUNKS = OUT_N / 8;  // 16-byte chunks per row
     const int n_out = EPI == IRIS_EPI_SILU_MUL ? N / 2 : N;
     const int col0 = tn * OUT_N;
+    if constexpr (EPI == kEpiQkRope) {
+      // Thread r normalises and rotates the Q / K heads of tile row r in place (two 128-column
+      // heads per row, 16 chunks each), then the tile leaves in 16-byte row chunks: Q / K rows to
+      // q / k at their token's position, the V columns to C.
+      static_assert(OUT_N == 256 && MASK == 15 && CHUNKS == 32, "two heads of 16 chunks per row");
+      const int nq = qk.heads * 128, nqk = nq + qk.kv_heads * 128;
+      const int rpb = job.group ? qk.rows_per_batch1 : qk.rows_per_batch0;
+      const int dst_offset = job.group ? qk.dst_offset1 : qk.dst_offset0;
+      if (tm * BM + tid < M) {
+        bf16* row = cl + tid * OUT_N;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int n0 = col0 + 128 * hh;  // (the same for the whole workgroup)
+          if (n0 >= n_out || n0 >= nqk) continue;
+          const float* gain = qk_gain + (n0 < nq ? 0 : 128);
+          auto chunk = [&](int c) { return reinterpret_cast<bf16x8*>(row + 8 * ((16 * hh + c) ^ (tid & MASK))); };
+          float ss[16];
+#pragma unroll
+          for (int c = 0; c < 16; ++c) {
+            const bf16x8 v = *chunk(c);
+            float a[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = to_f32(v[e]);
+            ss[c] = head_chunk_sq(a);
+          }
+          const float rs = head_rms_scale(head_sum_tree(ss), qk.eps);
+#pragma unroll
+          for (int c = 0; c < 16; ++c) {  // (read again: keeping the head in registers spills)
+            const bf16x8 v = *chunk(c);
+            float a[8], w[8], y[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = to_f32(v[e]);
+            load8(gain + 8 * c, w);
+            head_scale_rope(a, rs, w, qk_cos[c], qk_sin[c], y);
+            bf16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = from_f32<bf16>(y[e]);
+            *chunk(c) = o;
+          }
+        }
+      }
+      __syncthreads();
+      if (qk.vt) {
+        // V heads transposed: thread t gathers dim t % 128 for positions 8 c .. 8 c + 7 of the
+        // tile's tokens (each 16-position group in the slot order of vt_slot), c = t / 128 + 2 j;
+        // a wave's lanes read 64 consecutive dims of one tile row (no LDS bank conflicts) and
+        // store 16 bytes each into 64 rows of vt
+        const int b = (tm * BM) / rpb;
+        const long p0 = dst_offset + (tm * BM - b * rpb);  // a multiple of 16
+        const int d = tid & 127;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int n0 = col0 + 128 * hh;  // (the same for the whole workgroup)
+          if (n0 < nqk || n0 >= n_out) continue;
+          const int vh = (n0 - nqk) >> 7;
+          const int col = 128 * hh + d;
+          bf16* vtd = qk.vt + ((static_cast<long>(b) * qk.kv_heads + vh) * 128 + d) * static_cast<long>(qk.n_vt) + p0;
+#pragma unroll 4
+          for (int j = 0; j < 16; ++j) {
+            const int c8 = (tid >> 7) + 2 * j;  // (wave-uniform)
+            bf16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int i = vt_slot(8 * c8 + e);  // tile row holding this position's token
+              o[e] = cl[i * OUT_N + 4 * ((col >> 2) ^ (2 * (i & MASK))) + (col & 3)];
+            }
+            *reinterpret_cast<bf16x8*>(vtd + 8 * c8) = o;
+          }
+        }
+      }
+#pragma unroll 4
+      for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
+        const int r = idx / CHUNKS;
+        const int c = idx - r * CHUNKS;
+        const int m = tm * BM + r;
+        const int n0 = col0 + 8 * c;
+        if (m >= M || n0 >= n_out) continue;
+        if (n0 >= nqk && qk.vt) continue;  // (written transposed above)
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * OUT_N + 8 * (c ^ (r & MASK)));
+        if (n0 >= nqk) {  // V heads
+          *reinterpret_cast<bf16x8*>(C + static_cast<long>(m) * ldc + n0) = v;
+          continue;
+        }
+        const bool is_q = n0 < nq;
+        const int head = (is_q ? n0 : n0 - nq) >> 7;
+        const int b = m / rpb;
+        const long pos = dst_offset + (m - b * rpb);
+        bf16* dst = is_q ? qk.q + ((static_cast<long>(b) * qk.heads + head) * qk.n_dst + pos) * 128
+                         : qk.k + ((static_cast<long>(b) * qk.kv_heads + head) * qk.n_dst + pos) * 128;
+        *reinterpret_cast<bf16x8*>(dst + 8 * (c & 15)) = v;
+      }
+      return;
+    }
 #pragma unroll 4
     for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
       const int r = idx / CHUNKS;
@@ -423,7 +558,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmArgs p) {
   }
   wait_vmcnt<0>();
 
-  store_tile<BM, BN, WM, WN, FM, FN, NW, STAGES * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, [] {});
+  store_tile<BM, BN, WM, WN, FM, FN, NW, STAGES * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, p.qk, [] {});
 }
 
 // Instruction order of one k-step of gemm_w4_kernel: an MFMA, then the next k-step's NR
@@ -632,7 +767,7 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
   // the next tile's first K tile is in flight while this tile's output goes out
   const int next_tile = PERSIST ? persistent_tile(p, round + 1) : -1;
   const TileJob next = next_tile >= 0 ? locate_tile_at<BM, BN>(p, next_tile) : job;
-  store_tile<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, [&] {
+  store_tile<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, p.qk, [&] {
     if (next_tile >= 0) {
       set_rsrc(next);
       set_offsets(next);
@@ -692,6 +827,12 @@ int launch_w4(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
       gemm_w4_kernel<BM, IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, 0, stream>>>(args);
     else
       gemm_w4_kernel<BM, IRIS_EPI_SILU_MUL, float, false><<<all, 256, 0, stream>>>(args);
+  } else if (epilogue == kEpiQkRope) {
+    // one tile per workgroup: the next tile's loads in flight would spill the store's registers
+    if constexpr (BM == 256)
+      gemm_w4_kernel<BM, kEpiQkRope, bf16, false><<<all, 256, 0, stream>>>(args);
+    else
+      return fail(IRIS_E_UNSUPPORTED, "gemm: the q|k|v store runs on 256 x 256 tiles");
   } else {
     if (c_dtype == IRIS_BF16)
       gemm_w4_kernel<BM, IRIS_EPI_NONE, bf16, true><<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, 0,
@@ -824,8 +965,9 @@ thread_local int g_forced_tile = -1;
 // One launch over output columns [0, n) of operands already offset to the part's first column.
 int gemm_part(int groups, const void* const* a, const void* const* b, const float* const* bias, void* const* c,
               const int* m, int c_dtype, int n, int k, long lda, long ldb, long ldc, int epilogue, int tile,
-              hipStream_t stream) {
+              hipStream_t stream, const QkRope* qk = nullptr) {
   GemmArgs args{};
+  if (qk) args.qk = *qk;
   args.ngroups = groups;
   args.n = n;
   args.k = k;
@@ -932,6 +1074,73 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   }
   return gemm_part(groups, a, b2, bias ? bias2 : nullptr, c2, m, c_dtype, n - plan.n1, k, lda, ldb, ldc, epilogue,
                    plan.tile2, stream);
+}
+
+extern "C" int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const void* const* b, void* const* c,
+                                      const int* m, int n, int k, long lda, long ldb, long ldc,
+                                      const float* const* q_weight, const float* const* k_weight,
+                                      const int* rows_per_batch, const int* dst_offset, const float* cos_table,
+                                      const float* sin_table, long table_rows, void* q, void* k_out, int heads,
+                                      int kv_heads, long n_dst, void* vt, long n_vt, float eps, hipStream_t stream) {
+  IRIS_REQUIRE(groups == 1 || groups == 2, "gemm_qk_rope: 1 or 2 groups");
+  IRIS_REQUIRE(heads > 0 && kv_heads > 0 && n % 128 == 0 && n >= (heads + kv_heads) * 128,
+               "gemm_qk_rope: n (%d) must be whole 128-wide heads covering the %d Q and %d K heads", n, heads,
+               kv_heads);
+  IRIS_REQUIRE(k > 0 && k % kBK == 0, "gemm_qk_rope: need k > 0 and k %% 64 == 0 (got %d)", k);
+  IRIS_REQUIRE(lda >= k && ldb >= k && lda % 8 == 0 && ldb % 8 == 0, "gemm_qk_rope: lda/ldb must be >= k and multiples of 8");
+  IRIS_REQUIRE(ldc >= n && ldc % 8 == 0, "gemm_qk_rope: ldc must be >= n and a multiple of 8");
+  IRIS_REQUIRE(q && k_out && cos_table && sin_table && q_weight && k_weight && rows_per_batch && dst_offset,
+               "gemm_qk_rope: null pointer");
+  IRIS_REQUIRE(aligned(q, 16) && aligned(k_out, 16) && aligned(cos_table, 16) && aligned(sin_table, 16),
+               "gemm_qk_rope: q, k and the rotary tables must be 16-byte aligned");
+  IRIS_REQUIRE(n_dst > 0 && n_dst < (1L << 30) && table_rows > 0, "gemm_qk_rope: bad n_dst / table_rows");
+  for (int i = 0; i < groups; ++i) {
+    IRIS_REQUIRE(m[i] >= 0, "gemm_qk_rope: negative m");
+    if (m[i] == 0) continue;
+    IRIS_REQUIRE(a[i] && b[i] && c[i] && q_weight[i] && k_weight[i], "gemm_qk_rope: null pointer");
+    IRIS_REQUIRE(aligned(a[i], 16) && aligned(b[i], 16) && aligned(c[i], 16) && aligned(q_weight[i], 16) &&
+                     aligned(k_weight[i], 16),
+                 "gemm_qk_rope: operands and gains must be 16-byte aligned");
+    IRIS_REQUIRE(rows_per_batch[i] > 0 && m[i] % rows_per_batch[i] == 0,
+                 "gemm_qk_rope: m (%d) must be whole batch items of %d rows", m[i], rows_per_batch[i]);
+    IRIS_REQUIRE(dst_offset[i] >= 0 && dst_offset[i] + static_cast<long>(rows_per_batch[i]) <= n_dst &&
+                     dst_offset[i] + static_cast<long>(rows_per_batch[i]) <= table_rows,
+                 "gemm_qk_rope: positions %d..%d outside q/k (%ld) or the rotary table (%ld)", dst_offset[i],
+                 dst_offset[i] + rows_per_batch[i] - 1, n_dst, table_rows);
+    IRIS_REQUIRE(static_cast<long>(m[i]) * lda < (1L << 30), "gemm_qk_rope: activation above 2 GiB (32-bit byte offsets)");
+  }
+  IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 30), "gemm_qk_rope: weight above 2 GiB (32-bit byte offsets)");
+  if (vt) {
+    IRIS_REQUIRE(aligned(vt, 16) && n_vt > 0 && n_vt % 64 == 0 && n_vt < (1L << 30),
+                 "gemm_qk_rope: vt must be 16-byte aligned with n_vt a positive multiple of 64");
+    for (int i = 0; i < groups; ++i)
+      IRIS_REQUIRE(m[i] == 0 || (rows_per_batch[i] % 256 == 0 && dst_offset[i] % 16 == 0 &&
+                                 dst_offset[i] + static_cast<long>(rows_per_batch[i]) <= n_vt),
+                   "gemm_qk_rope: the V^T store needs rows_per_batch %% 256 == 0, dst_offset %% 16 == 0 and "
+                   "positions inside vt (group %d: %d rows at %d, n_vt %ld)",
+                   i, rows_per_batch[i], dst_offset[i], n_vt);
+  }
+  const int g1 = groups > 1 ? 1 : 0;
+  QkRope qk{};
+  qk.q = static_cast<bf16*>(q);
+  qk.k = static_cast<bf16*>(k_out);
+  qk.cos = cos_table;
+  qk.sin = sin_table;
+  qk.q_weight0 = q_weight[0];
+  qk.q_weight1 = q_weight[g1];
+  qk.k_weight0 = k_weight[0];
+  qk.k_weight1 = k_weight[g1];
+  qk.rows_per_batch0 = rows_per_batch[0];
+  qk.rows_per_batch1 = rows_per_batch[g1];
+  qk.dst_offset0 = dst_offset[0];
+  qk.dst_offset1 = dst_offset[g1];
+  qk.n_dst = static_cast<int>(n_dst);
+  qk.heads = heads;
+  qk.kv_heads = kv_heads;
+  qk.eps = eps;
+  qk.vt = static_cast<bf16*>(vt);
+  qk.n_vt = static_cast<int>(n_vt);
+  return gemm_part(groups, a, b, nullptr, c, m, IRIS_BF16, n, k, lda, ldb, ldc, kEpiQkRope, 11, stream, &qk);
 }
 
 extern "C" int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n,

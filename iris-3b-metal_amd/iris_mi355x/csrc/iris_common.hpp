@@ -111,6 +111,55 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Position of token slot i inside its group of 16 in the V^T layout the attention kernel reads:
+// the middle two 4-token quads are swapped (0-3, 8-11, 4-7, 12-15), so that the 8 keys one
+// MFMA lane needs (4 g .. 4 g + 3 and 8 + 4 g .. 8 + 4 g + 3) are contiguous. An involution.
+__device__ __forceinline__ int vt_slot(int i) {
+  const int quad = (i >> 2) & 3;
+  return (i & ~15) | ((quad == 1 ? 2 : quad == 2 ? 1 : quad) << 2) | (i & 3);
+}
+
+// Per-head RMSNorm + rotary embedding of one 128-wide head: y = rope((a / rms) * w), rms over
+// the 128 values (+ eps inside the root), pair j = (2 j, 2 j + 1) rotated by (c[j], s[j]) of its
+// position. The head is held as 16 chunks of 8 values (chunk s: elements 8 s .. 8 s + 7, rotary
+// pairs 4 s .. 4 s + 3); the squares are summed per chunk in element order, and the 16 chunk sums
+// combined as an xor butterfly over chunks 8, 4, 2, 1 apart (head_norm_rope: one chunk per lane
+// of an aligned 16-lane group, every lane of which must take part; head_sum_tree: the same
+// additions in one thread, equal bits).
+// (The fused multiply-adds are spelled out: left to contraction, the compiler fused a different
+// product of a two-product sum in different callers, one BF16 step apart now and then.)
+__device__ __forceinline__ float head_chunk_sq(const float (&a)[8]) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(a[e], a[e], ss);
+  return ss;
+}
+__device__ __forceinline__ float head_sum_tree(const float (&ss)[16]) {
+  float v1[8], v2[4], v3[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v1[i] = ss[i] + ss[i + 8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v2[i] = v1[i] + v1[i + 4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) v3[i] = v2[i] + v2[i + 2];
+  return v3[0] + v3[1];
+}
+__device__ __forceinline__ float head_rms_scale(float sum_sq, float eps) { return rsqrtf(sum_sq / 128.0f + eps); }
+__device__ __forceinline__ void head_scale_rope(const float (&a)[8], float r, const float (&w)[8], const f32x4& c,
+                                                const f32x4& s, float (&y)[8]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float a0 = (a[2 * p] * r) * w[2 * p];
+    const float a1 = (a[2 * p + 1] * r) * w[2 * p + 1];
+    y[2 * p] = __builtin_fmaf(a0, c[p], -(a1 * s[p]));
+    y[2 * p + 1] = __builtin_fmaf(a0, s[p], a1 * c[p]);
+  }
+}
+__device__ __forceinline__ void head_norm_rope(const float (&a)[8], const float (&w)[8], const f32x4& c,
+                                               const f32x4& s, float eps, float (&y)[8]) {
+  head_scale_rope(a, head_rms_scale(group_sum<16>(head_chunk_sq(a)), eps), w, c, s, y);
+}
+
 // x sigmoid(x) and sigmoid(x) with the hardware reciprocal (~1 ulp) in place of an IEEE division,
 // which costs about ten instructions per element in the GEMM and attention epilogues.
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }

@@ -252,19 +252,9 @@ __device__ __forceinline__ void qk_norm_rope_block(const TI* __restrict__ src, T
 #pragma unroll
   for (int k = 0; k < kQkRows; ++k) {
     const int head = head0 + k;
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += a[k][e] * a[k][e];
-    const float r = rsqrtf(group_sum<16>(ss) / 128.0f + eps);
-    if (head >= heads) continue;
     float y[8];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float a0 = (a[k][2 * p] * r) * w[2 * p];
-      const float a1 = (a[k][2 * p + 1] * r) * w[2 * p + 1];
-      y[2 * p] = a0 * c[p] - a1 * s[p];
-      y[2 * p + 1] = a0 * s[p] + a1 * c[p];
-    }
+    head_norm_rope(a[k], w, c, s, eps, y);  // all 16 lanes; clamped heads are not stored
+    if (head >= heads) continue;
     store8(dst + ((b * heads + head) * n_dst + out_token) * 128 + 8 * sub, y);
   }
 }
@@ -278,14 +268,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const TI* __restrict_
                                                            long col_offset, float eps) {
   qk_norm_rope_block<TI, TO>(src, dst, weight, cos_table, sin_table, n_src, n_dst, heads, dst_offset, row_stride,
                              col_offset, eps, blockIdx.x, blockIdx.y);
-}
-
-// Position of token slot i inside its group of 16 in the V^T layout the attention kernel reads:
-// the middle two 4-token quads are swapped (0-3, 8-11, 4-7, 12-15), so that the 8 keys one
-// MFMA lane needs (4 g .. 4 g + 3 and 8 + 4 g .. 8 + 4 g + 3) are contiguous. An involution.
-__device__ __forceinline__ int vt_slot(int i) {
-  const int quad = (i >> 2) & 3;
-  return (i & ~15) | ((quad == 1 ? 2 : quad == 2 ? 1 : quad) << 2) | (i & 3);
 }
 
 // Transpose the V heads into dst[b, h, d, position]: one workgroup per (64 output positions

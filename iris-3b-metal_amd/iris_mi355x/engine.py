@@ -13,7 +13,10 @@ accumulation; every activation crossing a GEMM is stored BF16 once.
 Data layout in HBM (per call shape, allocated once and reused):
 - dual-stream phase: image ``X`` ``[B*L, D]`` and text ``Y`` ``[B*T, D]`` FP32 residuals;
 - single-stream phase: ``tok`` ``[B*N, D]`` FP32 with the text rows first in each batch;
-- packed projections ``[rows, 6400]`` = ``q | k | v | gate`` (one GEMM per stream and block);
+- packed projections ``[rows, 6400]`` = ``q | k | v | gate``: two GEMMs per stream and block, the
+  q | k | v one writing the attention inputs below straight from its store (Q / K normed and
+  rotated; V transposed when each batch item is whole 256-row tiles, else its V columns land
+  here for ``v_heads_t``), the gate one its columns here;
 - attention inputs ``q`` ``[B, 20, N_pad, 128]``, ``k`` ``[B, 5, N_pad, 128]``, ``v^T`` ``[B, 5, 128, N_pad]``;
 - pixel stream ``[B*L, p*p, 16]`` FP32 and its BF16 normed copy, adaLN mods ``[B*L, p*p, 64]`` BF16.
 """
@@ -500,14 +503,21 @@ class HipIris:
         if not h_ready:
             K.rms_norm_modulate(X, blk["norm_x1"], xm[0], xm[1], eps, bf16, out=hx.view(B, Lp, D))
             K.rms_norm_modulate(Y, blk["norm_y1"], ym[0], ym[1], eps, bf16, out=hy.view(B, T, D))
-        K.linear_grouped([hx, hy], [blk["qkvg_x"], blk["qkvg_y"]], None, [px, py])
+        # q | k | v with the Q / K norm + rotary in the GEMM's store (text rows at positions 0.., image
+        # rows after them), the V heads transposed from its output, then the gate columns
         rope_c, rope_s = ws["rope"]
         q, k, vt = ws["q"], ws["k"], ws["vt"]
-        for proj, st, rows, off in ((py, "y", T, 0), (px, "x", Lp, T)):
-            pv = proj.view(B, rows, qkvg_w)
-            K.qkv_prepare(pv, blk[f"q_norm_{st}"], blk[f"k_norm_{st}"], rope_c, rope_s, eps, H, Hkv, q, k, vt,
-                          0, H * HEAD_DIM, (H + Hkv) * HEAD_DIM, off)
         gate_col = (H + 2 * Hkv) * HEAD_DIM
+        fuse_vt = Lp % 256 == 0 and T % 256 == 0  # whole 256-row tiles per item (and T % 16 == 0)
+        K.linear_qk_rope([hx, hy], [blk["qkvg_x"][:gate_col], blk["qkvg_y"][:gate_col]],
+                         [px[:, :gate_col], py[:, :gate_col]], [blk["q_norm_x"], blk["q_norm_y"]],
+                         [blk["k_norm_x"], blk["k_norm_y"]], rope_c, rope_s, eps, H, Hkv, q, k, [Lp, T], [T, 0],
+                         vt=vt if fuse_vt else None)
+        if not fuse_vt:
+            for proj, rows, off in ((py, T, 0), (px, Lp, T)):
+                K.v_heads_t(proj.view(B, rows, qkvg_w), Hkv, vt, (H + Hkv) * HEAD_DIM, off)
+        K.linear_grouped([hx, hy], [blk["qkvg_x"][gate_col:], blk["qkvg_y"][gate_col:]], None,
+                         [px[:, gate_col:], py[:, gate_col:]])
         K.flash_attention(q, k, vt, N, ay, ax, n_split=T, gate0=py[:, gate_col:], gate1=px[:, gate_col:])
         K.linear_grouped([ax, ay], [blk["proj_x_w"], blk["proj_y_w"]], [blk["proj_x_b"], blk["proj_y_b"]], [bx, by])
         K.gated_residual_grouped_([X, Y], [bx.view(B, Lp, D), by.view(B, T, D)],
@@ -540,13 +550,16 @@ class HipIris:
         qkvg_w = proj.shape[1]
         if not h_ready:
             K.rms_norm_modulate(tok.view(B, N, D), blk["norm1"], m[0], m[1], eps, torch.bfloat16, out=h.view(B, N, D))
-        K.linear(h, blk["qkvg"], out=proj)
         rope_c, rope_s = ws["rope"]
-        pv = proj.view(B, N, qkvg_w)
         q, k, vt = ws["q"], ws["k"], ws["vt"]
-        K.qkv_prepare(pv, blk["q_norm"], blk["k_norm"], rope_c, rope_s, eps, H, Hkv, q, k, vt,
-                      0, H * HEAD_DIM, (H + Hkv) * HEAD_DIM)
-        gate = proj[:, (H + 2 * Hkv) * HEAD_DIM:]
+        gate_col = (H + 2 * Hkv) * HEAD_DIM  # as in _dual_block
+        fuse_vt = N % 256 == 0
+        K.linear_qk_rope([h], [blk["qkvg"][:gate_col]], [proj[:, :gate_col]], [blk["q_norm"]], [blk["k_norm"]],
+                         rope_c, rope_s, eps, H, Hkv, q, k, [N], [0], vt=vt if fuse_vt else None)
+        if not fuse_vt:
+            K.v_heads_t(proj.view(B, N, qkvg_w), Hkv, vt, (H + Hkv) * HEAD_DIM)
+        gate = proj[:, gate_col:]
+        K.linear(h, blk["qkvg"][gate_col:], out=gate)
         if not last:
             R, M, per_batch = tok, rows, N
             attn = ws["attn"][:rows]

@@ -422,6 +422,63 @@ def linear_grouped(xs, weights, biases, outs, swiglu: bool = False) -> None:
     )
 
 
+def linear_qk_rope(xs, weights, outs, q_weights, k_weights, cos: torch.Tensor, sin: torch.Tensor, eps: float,
+                   heads: int, kv_heads: int, q: torch.Tensor, k: torch.Tensor, rows_per_batch, offsets,
+                   vt: torch.Tensor | None = None) -> None:
+    """``linear`` of one or two q | k | v projections (one per stream of a dual block, in one
+    launch) whose Q and K heads go to ``q`` / ``k`` normed and rotated exactly as ``qk_norm_rope``
+    writes them; the columns after them (the V heads) go to ``outs``, or with ``vt`` transposed
+    into it exactly as ``v_heads_t`` writes them (then ``outs`` is not written; every
+    ``rows_per_batch`` a multiple of 256 and every offset of 16). Group ``i``'s rows are batch
+    items of ``rows_per_batch[i]`` tokens, written at rows ``offsets[i] + token`` of ``q`` / ``k``
+    (``[B, heads, N, 128]`` / ``[B, kv_heads, N, 128]``, BF16) with gains ``q_weights[i]`` /
+    ``k_weights[i]`` and the rotary tables' rows ``offsets[i] + token``."""
+    groups = len(xs)
+    check = _Check("linear_qk_rope", q, k, cos, sin)
+    check(groups in (1, 2) and len(weights) == len(outs) == len(q_weights) == len(k_weights) == groups
+          and len(rows_per_batch) == len(offsets) == groups, "takes one or two problems")
+    kdim = xs[0].shape[-1]
+    n = weights[0].shape[0]
+    for x, w, o, rows in zip(xs, weights, outs, rows_per_batch):
+        c = _Check("linear_qk_rope", x, w, o)
+        c(x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and o.dtype == torch.bfloat16, "works on BF16")
+        c(w.shape == (n, kdim) and w.is_contiguous() and x.shape[-1] == kdim and x.stride(-1) == 1,
+          "shape mismatch")
+        c(o.shape[-1] == n and o.stride(-1) == 1 and o.reshape(-1, n).shape[0] == x.reshape(-1, kdim).shape[0],
+          "bad output")
+        c(rows > 0 and x.reshape(-1, kdim).shape[0] % rows == 0, "rows are not whole batch items")
+    x2 = [x.reshape(-1, kdim) for x in xs]
+    o2 = [o.reshape(-1, n) for o in outs]
+    check(all(x.stride(0) == x2[0].stride(0) for x in x2) and all(o.stride(0) == o2[0].stride(0) for o in o2),
+          "strides differ")
+    check(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and q.is_contiguous() and k.is_contiguous(),
+          "q / k must be contiguous BF16")
+    check(q.dim() == 4 and q.shape[1] == heads and q.shape[3] == HEAD_DIM
+          and k.shape == (q.shape[0], kv_heads, q.shape[2], HEAD_DIM),
+          "q / k must be [B, heads, N, 128] buffers of equal length")
+    check(cos.shape == sin.shape == (cos.shape[0], HEAD_DIM // 2), "rotary tables must be [N, 64]")
+    check.fp32(cos=cos, sin=sin, **{f"q_weight{i}": w for i, w in enumerate(q_weights)},
+               **{f"k_weight{i}": w for i, w in enumerate(k_weights)})
+    check(all(w.numel() == HEAD_DIM for w in (*q_weights, *k_weights)), "gains have 128 entries")
+    for x, rows in zip(x2, rows_per_batch):
+        check(x.shape[0] // rows <= q.shape[0], "more batch items than q / k hold")
+    if vt is not None:
+        check(vt.dtype == torch.bfloat16 and vt.is_contiguous() and vt.dim() == 4
+              and vt.shape[:3] == (q.shape[0], kv_heads, HEAD_DIM) and vt.shape[3] % 64 == 0,
+              f"vt must be a contiguous BF16 [{q.shape[0]}, {kv_heads}, 128, N] buffer, N % 64 == 0")
+        check(all(r % 256 == 0 and o % 16 == 0 for r, o in zip(rows_per_batch, offsets)),
+              "the V^T store needs rows_per_batch % 256 == 0 and offsets % 16 == 0")
+    L.call(
+        "iris_gemm_bf16_qk_rope", groups, L.pointer_array([L.ptr(x) for x in x2]),
+        L.pointer_array([L.ptr(w) for w in weights]), L.pointer_array([L.ptr(o) for o in o2]),
+        L.int_array([x.shape[0] for x in x2]), n, kdim, x2[0].stride(0), weights[0].stride(0), o2[0].stride(0),
+        L.pointer_array([L.ptr(w) for w in q_weights]), L.pointer_array([L.ptr(w) for w in k_weights]),
+        L.int_array(list(rows_per_batch)), L.int_array(list(offsets)), L.ptr(cos), L.ptr(sin), cos.shape[0],
+        L.ptr(q), L.ptr(k), heads, kv_heads, q.shape[2], L.ptr(vt), vt.shape[3] if vt is not None else 0,
+        float(eps), L.stream(),
+    )
+
+
 def pack_swiglu(w1: torch.Tensor, w3: torch.Tensor, hidden_pad: int) -> torch.Tensor:
     """Interleave SwiGLU ``w1``/``w3`` (``[H, D]``) in 32-row groups, zero-padded to ``hidden_pad``
     rows each: rows ``64p..64p+31`` are ``w1[32p:32p+32]``, rows ``64p+32..`` are ``w3[32p:..]``."""

@@ -155,6 +155,73 @@ def test_qkv_prepare_is_the_three_calls(heads, kv_heads, n_text, n_image):
     assert torch.all(bufs[1][0][:, :, n:] == 3.0) and torch.all(bufs[1][1][:, :, n:] == 3.0)
 
 
+@pytest.mark.parametrize("heads,kv_heads,rows,batch,kdim",
+                         [(20, 5, (4352,), 1, 2560), (20, 5, (4096, 256), 1, 2560), (3, 1, (400, 112), 2, 192)])
+def test_linear_qk_rope_is_linear_then_qkv_prepare(heads, kv_heads, rows, batch, kdim):
+    """The q | k | v GEMM with the Q / K norm + RoPE in its store writes bit for bit what the plain
+    GEMM followed by qkv_prepare writes (Q, K, and the V columns of the output): one group (the
+    single-stream block, 4352 tokens), two groups with the second's tokens first (a dual block's
+    image and text rows), and two batch items per group with tokens not a multiple of the tile.
+    Other q / k rows and the Q / K columns of the output are left as they were."""
+    g = torch.Generator(device=DEV).manual_seed(31)
+    n = (heads + 2 * kv_heads) * 128
+    v_col = (heads + kv_heads) * 128
+    tokens = [r // batch for r in rows]
+    offsets = [tokens[1], 0] if len(rows) == 2 else [0]
+    n_pad = (sum(tokens) + 63) // 64 * 64 + 64
+    cos = torch.randn(n_pad, 64, generator=g, device=DEV)
+    sin = torch.randn(n_pad, 64, generator=g, device=DEV)
+    xs = [(0.5 * torch.randn(r, kdim, generator=g, device=DEV)).to(torch.bfloat16) for r in rows]
+    ws = [(0.05 * torch.randn(n, kdim, generator=g, device=DEV)).to(torch.bfloat16) for _ in rows]
+    qws = [1 + 0.1 * torch.randn(128, generator=g, device=DEV) for _ in rows]
+    kws = [1 + 0.1 * torch.randn(128, generator=g, device=DEV) for _ in rows]
+
+    def buffers():
+        return (torch.full((batch, heads, n_pad, 128), 3.0, device=DEV, dtype=torch.bfloat16),
+                torch.full((batch, kv_heads, n_pad, 128), 3.0, device=DEV, dtype=torch.bfloat16))
+
+    q_ref, k_ref = buffers()
+    vt = torch.zeros(batch, kv_heads, 128, n_pad, device=DEV, dtype=torch.bfloat16)
+    _lib.call("iris_gemm_force_tile", 11)
+    try:
+        outs_ref = [K.linear(x, w) for x, w in zip(xs, ws)]
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    for out, qw, kw, tok, off in zip(outs_ref, qws, kws, tokens, offsets):
+        K.qkv_prepare(out.view(batch, tok, n), qw, kw, cos, sin, 1e-6, heads, kv_heads, q_ref, k_ref, vt, 0,
+                      heads * 128, v_col, off)
+    q, k = buffers()
+    outs = [torch.full((r, n), 5.0, device=DEV, dtype=torch.bfloat16) for r in rows]
+    K.linear_qk_rope(xs, ws, outs, qws, kws, cos, sin, 1e-6, heads, kv_heads, q, k, tokens, offsets)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_ref) and torch.equal(k, k_ref)
+    for out, ref in zip(outs, outs_ref):
+        assert torch.equal(out[:, v_col:], ref[:, v_col:])
+        assert torch.all(out[:, :v_col] == 5.0)
+    if all(t % 256 == 0 for t in tokens):  # the V heads straight into the V^T layout as well
+        q, k = buffers()
+        vt2 = torch.zeros_like(vt)
+        outs = [torch.full((r, n), 5.0, device=DEV, dtype=torch.bfloat16) for r in rows]
+        K.linear_qk_rope(xs, ws, outs, qws, kws, cos, sin, 1e-6, heads, kv_heads, q, k, tokens, offsets, vt=vt2)
+        torch.cuda.synchronize()
+        assert torch.equal(q, q_ref) and torch.equal(k, k_ref) and torch.equal(vt2, vt)
+        assert all(torch.all(out == 5.0) for out in outs)
+
+
+def test_linear_qk_rope_rejects_bad_layouts():
+    """Host checks before any launch: rows that are not whole batch items, positions past q / k."""
+    x = torch.zeros(100, 128, device=DEV, dtype=torch.bfloat16)
+    w = torch.zeros(3 * 128, 128, device=DEV, dtype=torch.bfloat16)
+    out = torch.zeros(100, 3 * 128, device=DEV, dtype=torch.bfloat16)
+    gain = torch.ones(128, device=DEV)
+    cos = torch.zeros(128, 64, device=DEV)
+    q = torch.zeros(1, 1, 128, 128, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="whole batch items"):
+        K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [30], [0])
+    with pytest.raises(ValueError, match="outside q/k"):
+        K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [100], [40])
+
+
 @pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
 def test_qk_norm_rope_trunk_shape_matches_oracle(src_dtype):
     """The single-stream block's Q (20 heads) and K (5 heads) of 256 text + 4096 image tokens,
