@@ -940,11 +940,12 @@ struct SplitPlan {
 };
 SplitPlan plan_split(const int* m, int groups, int n, int epilogue, int forced) {
   SplitPlan plan;
-  if (forced >= 0) return plan;
+  const Candidate& c11 = kCandidates[0];
+  // the first part always runs on tile 11: no split for an epilogue that tile does not have
+  if (forced >= 0 || !allowed(c11, epilogue)) return plan;
   double whole = 0.0;
   plan.tile1 = pick_tile(m, groups, n, epilogue, -1, &whole);
   const int cus = device_cus();
-  const Candidate& c11 = kCandidates[0];
   const double extra_launch = 65536.0 / c11.rate * 0.05;
   double best = 0.98 * whole;  // a split must win by 2%
   for (int c = 1; c * 256 < n; ++c) {
@@ -1111,6 +1112,10 @@ extern "C" int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const vo
   }
   IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 30), "gemm_qk_rope: weight above 2 GiB (32-bit byte offsets)");
   if (vt) {
+    // every column past the Q / K heads is a V head of vt: exactly kv_heads of them
+    IRIS_REQUIRE(n == (heads + 2 * kv_heads) * 128,
+                 "gemm_qk_rope: with vt, n (%d) must be exactly the %d Q, %d K and %d V heads of 128 columns", n,
+                 heads, kv_heads, kv_heads);
     IRIS_REQUIRE(aligned(vt, 16) && n_vt > 0 && n_vt % 64 == 0 && n_vt < (1L << 30),
                  "gemm_qk_rope: vt must be 16-byte aligned with n_vt a positive multiple of 64");
     for (int i = 0; i < groups; ++i)

@@ -468,6 +468,9 @@ def linear_qk_rope(xs, weights, outs, q_weights, k_weights, cos: torch.Tensor, s
               f"vt must be a contiguous BF16 [{q.shape[0]}, {kv_heads}, 128, N] buffer, N % 64 == 0")
         check(all(r % 256 == 0 and o % 16 == 0 for r, o in zip(rows_per_batch, offsets)),
               "the V^T store needs rows_per_batch % 256 == 0 and offsets % 16 == 0")
+        check(n == (heads + 2 * kv_heads) * HEAD_DIM,
+              f"with vt the weight must hold exactly {heads} Q, {kv_heads} K and {kv_heads} V heads "
+              f"({(heads + 2 * kv_heads) * HEAD_DIM} rows), got {n}")
     L.call(
         "iris_gemm_bf16_qk_rope", groups, L.pointer_array([L.ptr(x) for x in x2]),
         L.pointer_array([L.ptr(w) for w in weights]), L.pointer_array([L.ptr(o) for o in o2]),

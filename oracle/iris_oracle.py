@@ -18,13 +18,16 @@ unmodified ``iris3b.nn`` modules. The blocks ``mmdit_block``,
 unmodified reference block modules (blocks/mmdit.py, single_stream.py,
 pit.py, loaded by file path) at the released topology and the tiny config.
 The reference's ``IrisDiT`` itself cannot be imported here (its config module
-needs omegaconf, which is absent), so the glue of ``forward`` that lives only
-in src/iris3b/models/dit.py:283-375 is "parity unpinned" beyond the
-reference's invariants (adaLN identity, keep/drop equality, zero head,
-parameter count) and unfold/fold: ``cond = silu(t_emb)``, the
-``y_pos_embedding`` add of ``embed_text``, the block loop's hand-over of
-``[text | image]`` rows, the ``silu(t_emb + s)`` re-fusion, and the
-``FinalLayer`` (RMSNorm then Linear).
+needs omegaconf, which is absent); the glue of ``forward`` and ``embed_text``
+that lives only in src/iris3b/models/dit.py:263-375 (``cond = silu(t_emb)``,
+text truncation and the ``y_pos_embedding`` add, the block loop's hand-over
+of ``[text | image]`` rows, the ``silu(t_emb + s)`` re-fusion, the
+``FinalLayer`` RMSNorm then Linear, the fold) is pinned by closed-form
+known answers at the released topology and the tiny config
+(``tests/test_oracle_forward_glue.py``): weights that make every attention
+uniform and every PiT branch a plain shift or bias give a flow computed from
+library routines and golden-pinned layers alone, and each plausible mistake
+written into a copy of this module's source fails that comparison.
 The downstream wrappers ``depth_forward`` and ``restore_tile`` are pinned by
 invariants of their own (``tests/test_tasks.py``): the zero fourth channel
 equals the three-channel model with the sliced embedders, and a head that

@@ -164,6 +164,53 @@ def test_iris3b_shallow_forward_at_256px_matches_oracle(iris3b_blocks, batch, hw
     check(got, want, f"iris3b shallow B={batch} {hw} T={n_text}")
 
 
+def _bf16_attention(q, k, v, mask=None):
+    """The oracle's attention on operands rounded to BF16, as the HIP path stores them."""
+    r = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    return _ORACLE_ATTENTION(r(q), r(k), r(v), mask)
+
+
+_ORACLE_ATTENTION = O.attention
+
+
+@pytest.mark.parametrize("gain", [4.0, 27.0])
+def test_iris3b_forward_at_1024_with_large_late_qk_gains(iris3b_blocks, gain, monkeypatch):
+    """Full-width Iris-3B (1 dual + 1 single + 1 pixel block) at 1024x1024 with 256 text tokens,
+    the last (single-stream) block's q_norm / k_norm gains raised to ``gain`` (the released
+    model's late single-stream blocks reach 27): attention logits of standard deviation up to
+    gain^2. BF16 attention operands alone then move the output away from the FP32 forward by
+    more than the end-to-end bar (rounding Q and K to BF16 at gain 27 is ~1 nat of logit noise):
+    the oracle evaluated with its attention operands rounded to BF16 measures that floor. The
+    HIP forward must meet the end-to-end bar, or else stay within 3x of that floor (cosine
+    deficit and max-rel), which a wrong rescale or a dropped tile in the softmax's raise path
+    would exceed by orders of magnitude."""
+    from parity import COS_MIN, MAX_REL, metrics
+
+    cfg, sd = iris3b_blocks
+    sd = dict(sd)
+    last = f"blocks.{cfg.depth - 1}"
+    g = torch.Generator().manual_seed(27)
+    for name in ("q_norm", "k_norm"):
+        sd[f"{last}.{name}.weight"] = gain * (1 + 0.02 * torch.randn(cfg.head_dim, generator=g))
+    x = torch.randn(1, 3, 1024, 1024, generator=g)
+    t = torch.tensor([600.0])
+    text = torch.randn(1, 256, cfg.hidden_size, generator=g)
+    engine = HipIris(cfg, sd, device=DEV)
+    got = engine(x.to(DEV), t.to(DEV), text.to(DEV)).cpu()
+    _all_cores()
+    want = O.forward(sd, cfg, x, t, prepared_text=text)
+    monkeypatch.setattr(O, "attention", _bf16_attention)
+    floor = O.forward(sd, cfg, x, t, prepared_text=text)
+    cos, max_rel = metrics(got, want)
+    cos_f, max_rel_f = metrics(floor, want)
+    print(f"gain {gain}: HIP cosine {cos:.7f} max-rel {max_rel:.3e}; BF16-operand oracle cosine {cos_f:.7f} "
+          f"max-rel {max_rel_f:.3e}", flush=True)
+    assert torch.isfinite(got).all()
+    at_bar = cos >= COS_MIN and max_rel <= MAX_REL
+    at_floor = (1 - cos) <= 3 * (1 - cos_f) and max_rel <= 3 * max_rel_f
+    assert at_bar or at_floor, (cos, max_rel, cos_f, max_rel_f)
+
+
 def test_iris3b_encode_text_matches_oracle(iris3b_blocks):
     """Full-width adapter: 12 encoder layers of 2560 (32 heads of 80), MLP 3328, refiner of 20
     heads of 128 with SwiGLU 6826, 300 text tokens of which 123 are real."""

@@ -3,6 +3,8 @@ on seeded inputs. Tolerances: FP32 outputs to FP32 rounding (summation order dif
 BF16 outputs to one BF16 rounding of the FP32 result; MFMA products to the BF16 operand
 rounding they are specified with (FP32 accumulation)."""
 
+import math
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -220,6 +222,23 @@ def test_linear_qk_rope_rejects_bad_layouts():
         K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [30], [0])
     with pytest.raises(ValueError, match="outside q/k"):
         K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [100], [40])
+    # with vt every column past the Q / K heads is a V head: a q | k | v | gate weight (one head of
+    # each) would write its gate columns past vt's single V head
+    x = torch.zeros(256, 128, device=DEV, dtype=torch.bfloat16)
+    w = torch.zeros(4 * 128, 128, device=DEV, dtype=torch.bfloat16)
+    out = torch.zeros(256, 4 * 128, device=DEV, dtype=torch.bfloat16)
+    cos = torch.zeros(256, 64, device=DEV)
+    q = torch.zeros(1, 1, 256, 128, device=DEV, dtype=torch.bfloat16)
+    vt = torch.zeros(1, 1, 128, 256, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="exactly"):
+        K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [256], [0], vt=vt)
+    # the C entry point refuses it on its own (IRIS_E_INVALID), whatever the caller checked
+    with pytest.raises(ValueError, match="exactly"):
+        _lib.call("iris_gemm_bf16_qk_rope", 1, _lib.pointer_array([x.data_ptr()]), _lib.pointer_array([w.data_ptr()]),
+                  _lib.pointer_array([out.data_ptr()]), _lib.int_array([256]), 4 * 128, 128, 128, 128, 4 * 128,
+                  _lib.pointer_array([gain.data_ptr()]), _lib.pointer_array([gain.data_ptr()]),
+                  _lib.int_array([256]), _lib.int_array([0]), cos.data_ptr(), cos.data_ptr(), 256, q.data_ptr(),
+                  q.clone().data_ptr(), 1, 1, 256, vt.data_ptr(), 256, 1e-6, _lib.stream())
 
 
 @pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
@@ -554,6 +573,118 @@ def test_flash_attention_trunk_shape_with_gate_and_split():
         close_attention(got[sel, hh] / gates, plain)  # the gate does not hide an error
 
 
+# -- attention at the magnitudes of the trained model -----------------------------------------
+# Late single-stream blocks of the released model carry QK-norm gains up to ~27, so their
+# attention logits reach hundreds of nats. The kernels' softmax keeps a lazy running max per
+# query column that moves only when a probability would exceed 2^8 (a score ~5.5 nats above it);
+# these inputs drive that path in most tiles, each in a different way:
+# - "gainG": Q and K as the per-head RMSNorm leaves them (unit RMS) times a gain G: logits of
+#   standard deviation G^2 (4, 27^2); the larger ones make the softmax nearly one-hot;
+# - "ramp": every query along one direction with its own length, key j along it in proportion
+#   to j: each query's logits climb 2-10 nats per 32 keys, so its max moves in nearly every tile
+#   and the earlier tiles' output must be rescaled each time;
+# - "last_key_peak": N(0,1)-scale logits except the last key, ~ln(n) + 2 above the rest for
+#   every query: a raise in the very last tile that rescales the ~12% of the weight
+#   accumulated before it.
+LOGIT_MODES = ["gain2", "gain27", "ramp", "last_key_peak"]
+
+
+def _logit_inputs(b, h, hkv, n, seed, mode):
+    g = gen(seed)
+    q = torch.randn(b, h, n, 128, generator=g)
+    k = torch.randn(b, hkv, n, 128, generator=g)
+    v = torch.randn(b, hkv, n, 128, generator=g)
+    e = F.normalize(torch.randn(128, generator=g), dim=0)
+    if mode.startswith("gain"):
+        gain = float(mode[4:])
+        q, k = q * gain, k * gain
+    elif mode == "ramp":
+        length = 2.0 + 8.0 * torch.rand(b, h, n, 1, generator=g)
+        q = length * e + 0.02 * q
+        k = 0.354 * torch.arange(n, dtype=torch.float32)[:, None] * e + 0.5 * k
+    elif mode == "last_key_peak":
+        q = 0.7 * q + 3.0 * e
+        k[:, :, n - 1] = (math.log(n) + 2.0) * math.sqrt(128) / 3.0 * e
+    else:
+        raise ValueError(mode)
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    n_pad = (n + 63) // 64 * 64
+    qd = torch.zeros(b, h, n_pad, 128, dtype=torch.bfloat16)
+    kd = torch.zeros(b, hkv, n_pad, 128, dtype=torch.bfloat16)
+    vt = torch.zeros(b, hkv, 128, n_pad, dtype=torch.bfloat16)
+    qd[:, :, :n], kd[:, :, :n], vt[..., :n] = q, k, v.transpose(-1, -2)
+    vt = vt[..., K.vt_positions(n_pad)].contiguous()
+    return q, k, v, qd.to(DEV), kd.to(DEV), vt.to(DEV)
+
+
+def _peak_weight(q, k, hh, hkv_per):
+    """Largest softmax weight per query row of head hh (how one-hot the inputs make it)."""
+    s = q[0, hh].float() @ k[0, hh // hkv_per].float().T / math.sqrt(128)
+    return torch.softmax(s, -1).max(-1).values
+
+
+@pytest.mark.parametrize("mode", LOGIT_MODES)
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+def test_flash_attention_large_logits(variant, mode):
+    """Every variant (64-key register-staged, 32-key register-staged, 64-key ring, 32-key ring,
+    twelve-wave ring) against the FP32 oracle on the same BF16 inputs at large logits."""
+    b, h, hkv, n = 2, 8, 2, 333
+    q, k, v, qd, kd, vt = _logit_inputs(b, h, hkv, n, 40 + LOGIT_MODES.index(mode), mode)
+    want = O.attention(q.float(), k.float(), v.float()).transpose(1, 2).reshape(b, n, h * 128)
+    out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+    _lib.call("iris_flash_attn_force_variant", variant)
+    try:
+        K.flash_attention(qd, kd, vt, n, None, out, n_split=0)
+    finally:
+        _lib.call("iris_flash_attn_force_variant", -1)
+    got = out.view(b, n, -1)
+    assert torch.isfinite(got.float()).all()
+    close_attention(got, want)
+    if mode == "gain27":  # nearly one-hot: most rows are one value row, to BF16 rounding
+        assert _peak_weight(q, k, 0, h // hkv).median() > 0.99
+
+
+@pytest.mark.parametrize("mode", LOGIT_MODES)
+def test_flash_attention_trunk_shape_large_logits(mode):
+    """The trunk shape (20 query / 5 K/V heads over 256 text + 4096 image tokens, gate fused, rows
+    split) at large logits, on the automatic variant choice."""
+    b, h, hkv, t, l = 1, 20, 5, 256, 4096
+    n = t + l
+    q, k, v, qd, kd, vt = _logit_inputs(b, h, hkv, n, 50 + LOGIT_MODES.index(mode), mode)
+    gate = torch.randn(n, h * 128, generator=gen(10)).to(torch.bfloat16)
+    oy = torch.zeros(t, h * 128, device=DEV, dtype=torch.bfloat16)
+    ox = torch.zeros(l, h * 128, device=DEV, dtype=torch.bfloat16)
+    gd = gate.to(DEV)
+    K.flash_attention(qd, kd, vt, n, oy, ox, n_split=t, gate0=gd[:t], gate1=gd[t:])
+    got = torch.cat([oy, ox]).float().cpu().view(n, h, 128)
+    assert torch.isfinite(got).all()
+    sel = torch.cat([torch.arange(0, t, 5), torch.arange(t, n, 11)])
+    for hh in (0, 7, 19):
+        qh = q[:, hh:hh + 1, sel].float()
+        plain = O.attention(qh, k[:, hh // 4:hh // 4 + 1].float(), v[:, hh // 4:hh // 4 + 1].float())[0, 0]
+        gates = torch.sigmoid(gate[sel, hh * 128:(hh + 1) * 128].float())
+        close_attention(got[sel, hh] / gates, plain)
+
+
+@pytest.mark.parametrize("mode", ["gain27", "ramp"])
+def test_flash_attention_masked_large_logits(mode):
+    """The text refiner's masked attention (pad keys dropped, each query keeps its own key) at large
+    logits, including an all-pad prompt and padding keys at the start."""
+    b, h, n = 3, 4, 130
+    q, k, v, qd, kd, vt = _logit_inputs(b, h, h, n, 60, mode)
+    n_pad = qd.shape[2]
+    mask = _text_mask(b, n + 5, n, 12, torch.int64)
+    keep = mask[:, :n].bool()[:, None, None, :] | torch.eye(n, dtype=torch.bool)
+    want = O.attention(q.float(), k.float(), v.float(), keep).transpose(1, 2).reshape(b, n, h * 128)
+    km = torch.zeros(b, n_pad, device=DEV, dtype=torch.uint8)
+    K.text_key_mask(mask.to(DEV), n, km)
+    out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+    K.flash_attention_masked(qd, kd, vt, n, km, out)
+    got = out.view(b, n, -1)
+    assert torch.isfinite(got.float()).all()
+    close_bf16(got, want, scale=1.0, floor=4e-3)
+
+
 # -- text adapter ---------------------------------------------------------------------------
 @pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 def test_gemm_silu_epilogue(tile):
@@ -573,6 +704,21 @@ def test_gemm_silu_epilogue(tile):
         want = F.silu(_gemm_ref(a, w, bias))
         torch.testing.assert_close(out32.cpu(), want, rtol=1e-4, atol=1e-4)
         close_bf16(out16, want)
+
+
+@pytest.mark.parametrize("m", [6144, 6912, 12288])
+def test_gemm_silu_epilogue_at_batched_adapter_shapes(m):
+    """Linear + SiLU of the layer-wise blocks' MLP at full width for batched prompts (2 x 256,
+    2 x 288 and 4 x 256 tokens x 12 layers): shapes whose automatic tile choice weighs a column
+    split, which must not put the SiLU epilogue on a tile that lacks it."""
+    g = gen(22)
+    n, k = 3328, 2560
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, generator=g)).to(torch.bfloat16)
+    bias = 0.1 * torch.randn(n, generator=g)
+    out16 = K.linear(a.to(DEV), w.to(DEV), bias.to(DEV), silu=True)
+    want = F.silu(_gemm_ref(a, w, bias))
+    close_bf16(out16, want)
 
 
 def test_gemm_silu_is_refused_by_the_four_wave_tile():
