@@ -352,14 +352,18 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][qb][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_max = fmaxf(m_run[qb], mx * sl2);
-        // (a column with no key so far takes a finite reference, so masked tiles give 0, not NaN)
-        const float m_new = !raise ? m_run[qb] : (MASKED && m_max == -INFINITY ? 0.0f : m_max);
-        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);  // exactly 1 unless raised
+        const float m_new = !raise ? m_run[qb] : m_max;
+        // A masked column with no key so far keeps max -inf (so that its first key, however low
+        // its score, raises it: a finite stand-in would let every later probability underflow
+        // to 0 and leave the row 0 / 0), and its all-masked tiles are evaluated against 0,
+        // which gives exact zeros instead of NaN.
+        const float m_ref = MASKED && m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_ref);  // exactly 1 unless raised
         l_run[qb] *= alpha;
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[db][qb] *= alpha;
         m_run[qb] = m_new;
-        sum = probs(qb, m_new);
+        sum = probs(qb, m_ref);
       }
       l_run[qb] += sum;
     }

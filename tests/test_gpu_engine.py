@@ -164,10 +164,20 @@ def test_iris3b_shallow_forward_at_256px_matches_oracle(iris3b_blocks, batch, hw
     check(got, want, f"iris3b shallow B={batch} {hw} T={n_text}")
 
 
+def _bf16(t):
+    return t.to(torch.bfloat16).float()
+
+
 def _bf16_attention(q, k, v, mask=None):
     """The oracle's attention on operands rounded to BF16, as the HIP path stores them."""
-    r = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
-    return _ORACLE_ATTENTION(r(q), r(k), r(v), mask)
+    return _ORACLE_ATTENTION(_bf16(q), _bf16(k), _bf16(v), mask)
+
+
+def _bf16_linear(p, name, x):
+    """The oracle's Linear at the HIP path's rounding points: BF16 weights and inputs, FP32
+    accumulation and bias, the output rounded to BF16."""
+    b = p.get(f"{name}.bias")
+    return _bf16(torch.nn.functional.linear(_bf16(x), _bf16(p[f"{name}.weight"]), b))
 
 
 _ORACLE_ATTENTION = O.attention
@@ -178,10 +188,11 @@ def test_iris3b_forward_at_1024_with_large_late_qk_gains(iris3b_blocks, gain, mo
     """Full-width Iris-3B (1 dual + 1 single + 1 pixel block) at 1024x1024 with 256 text tokens,
     the last (single-stream) block's q_norm / k_norm gains raised to ``gain`` (the released
     model's late single-stream blocks reach 27): attention logits of standard deviation up to
-    gain^2. BF16 attention operands alone then move the output away from the FP32 forward by
-    more than the end-to-end bar (rounding Q and K to BF16 at gain 27 is ~1 nat of logit noise):
-    the oracle evaluated with its attention operands rounded to BF16 measures that floor. The
-    HIP forward must meet the end-to-end bar, or else stay within 3x of that floor (cosine
+    gain^2. BF16 operands then move the output away from the FP32 forward by more than the
+    end-to-end bar (rounding Q and K to BF16 at gain 27 is ~1 nat of logit noise): the oracle
+    evaluated at the HIP path's rounding points (BF16 weights, Linear inputs and outputs and
+    attention operands; FP32 accumulation, norms, softmax and residuals) measures that floor.
+    The HIP forward must meet the end-to-end bar, or else stay within 3x of that floor (cosine
     deficit and max-rel), which a wrong rescale or a dropped tile in the softmax's raise path
     would exceed by orders of magnitude."""
     from parity import COS_MIN, MAX_REL, metrics
@@ -200,10 +211,11 @@ def test_iris3b_forward_at_1024_with_large_late_qk_gains(iris3b_blocks, gain, mo
     _all_cores()
     want = O.forward(sd, cfg, x, t, prepared_text=text)
     monkeypatch.setattr(O, "attention", _bf16_attention)
+    monkeypatch.setattr(O, "linear", _bf16_linear)
     floor = O.forward(sd, cfg, x, t, prepared_text=text)
     cos, max_rel = metrics(got, want)
     cos_f, max_rel_f = metrics(floor, want)
-    print(f"gain {gain}: HIP cosine {cos:.7f} max-rel {max_rel:.3e}; BF16-operand oracle cosine {cos_f:.7f} "
+    print(f"gain {gain}: HIP cosine {cos:.7f} max-rel {max_rel:.3e}; oracle at BF16 rounding points cosine {cos_f:.7f} "
           f"max-rel {max_rel_f:.3e}", flush=True)
     assert torch.isfinite(got).all()
     at_bar = cos >= COS_MIN and max_rel <= MAX_REL
