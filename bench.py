@@ -115,24 +115,24 @@ class LaunchTimer:
         orig_linear, orig_grouped = K.linear, K.linear_grouped
         timer = self
 
-        def linear(x, weight, bias=None, out=None, out_dtype=torch.bfloat16, swiglu=False, silu=False):
+        def linear(x, weight, bias=None, out=None, out_dtype=torch.bfloat16, swiglu=False, silu=False, **kw):
             if not timer.enabled:
-                return orig_linear(x, weight, bias, out, out_dtype, swiglu, silu)
+                return orig_linear(x, weight, bias, out, out_dtype, swiglu, silu, **kw)
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
-            res = orig_linear(x, weight, bias, out, out_dtype, swiglu, silu)
+            res = orig_linear(x, weight, bias, out, out_dtype, swiglu, silu, **kw)
             e.record()
             m = x.numel() // x.shape[-1]
             k = x.shape[-1] if x.shape[-1] != timer.patch_k else 3 * timer.cfg.patch_size ** 2
             timer.records.append((s, e, timer.flops(m, weight.shape[0], k, swiglu), swiglu))
             return res
 
-        def linear_grouped(xs, weights, biases, outs, swiglu=False):
+        def linear_grouped(xs, weights, biases, outs, swiglu=False, **kw):
             if not timer.enabled:
-                return orig_grouped(xs, weights, biases, outs, swiglu)
+                return orig_grouped(xs, weights, biases, outs, swiglu, **kw)
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
-            orig_grouped(xs, weights, biases, outs, swiglu)
+            orig_grouped(xs, weights, biases, outs, swiglu, **kw)
             e.record()
             fl = sum(timer.flops(x.numel() // x.shape[-1], w.shape[0], x.shape[-1], swiglu) for x, w in zip(xs, weights))
             timer.records.append((s, e, fl, swiglu))
@@ -426,7 +426,7 @@ def main() -> None:
     roofline = {"bound": "mfma", "kernel": "gemm_w4_kernel<256, SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
                 **rate(True), "traffic": profiled_traffic(),
                 "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
-    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel incl. the q|k|v store with Q/K norm + RoPE, gemm_kernel, hipBLASLt for the plain shapes)", **rate(False)}
+    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel incl. the q|k|v store with Q/K norm + RoPE, gemm_kernel)", **rate(False)}
     att_source = ATTENTION_TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if ATTENTION_TRAFFIC_PROFILE.exists() else None
     attention = {"kernel": "flash_attn_kernel, trunk joint attention (20 query / 5 K/V heads)",
                  **timer.attention_summary(cfg.num_heads),

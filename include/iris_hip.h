@@ -166,14 +166,9 @@ int iris_layer_pool(const float* h, const void* branch, const float* weight, con
  * IRIS_EPI_SILU: C = silu(A B^T + bias) (the Linear + SiLU of the layer-wise text adapter's
  * MLP, src/iris3b/nn/embeddings.py:131-135). Operands are addressed with 32-bit byte offsets:
  * m * lda and n * ldb below 2^30 elements (2 GiB), else IRIS_E_INVALID before any launch.
- * Plain products (IRIS_EPI_NONE, BF16 output) of the weight shapes n x k = 2560 x 6848,
- * 16384 x 2560, 1280 x 4096, 3840 x 1280, 1280 x 1280 and 4096 x 1280 at 2048 rows or more run
- * on hipBLASLt (measured faster in the denoise step, algorithms that take no workspace); the
- * first call of such a problem on a device creates a hipBLASLt handle and the problem's plan, so
- * it must not be made while the stream is being captured into a graph (it then runs this
- * library's kernel instead).
- * Its rounding order follows the row count: call one batch item at a time where rows must not
- * depend on the batch. */
+ * Every output element is the FP32 sum over k in increasing order whatever m and the tile
+ * choice, so a row's result does not depend on the other rows. Stateless: no allocation, no
+ * host synchronisation, safe to record in a graph. */
 int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n, int k,
                    long lda, long ldb, long ldc, int epilogue, hipStream_t stream);
 
@@ -181,8 +176,7 @@ int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int
  * iris_gemm_bf16* calls made by the calling thread (an index into the tile table of gemm.hip:
  * 0-10 tiles of 256x256, 256x192, 192x256 and 128x128 for the kernel with direct-to-LDS
  * refills; 11 and 12 the four-wave kernel with register-staged refills at 256x256 and 192x256,
- * the automatic choice for most shapes) or restore the automatic choice (-1). A forced tile
- * also keeps the hipBLASLt shapes on this library's kernels.
+ * the automatic choice for most shapes) or restore the automatic choice (-1).
  * The setting is per thread. No counterpart in the reference. */
 int iris_gemm_force_tile(int tile);
 

@@ -62,8 +62,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(compile_one, srcs))
     tmp = LIBRARY.with_suffix(".so.tmp")
-    # hipBLASLt runs the plain GEMMs listed in csrc/blaslt.hip
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-lhipblaslt", "-o", str(tmp)]
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link of libiris_hip.so failed:\n{res.stderr}")

@@ -15,7 +15,6 @@
 // wait + barrier for the next K tile is placed before the last k-step of the current one.
 // Workgroup ids are remapped so that the tiles running concurrently on one XCD form an
 // 8 x 4 block and share their operands through that XCD's L2.
-#include "blaslt.hpp"
 #include "iris_common.hpp"
 
 #include <type_traits>
@@ -1048,13 +1047,6 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 30), "gemm: weight above 2 GiB (32-bit byte offsets)");
   for (int i = 0; i < groups; ++i)
     IRIS_REQUIRE(static_cast<long>(m[i]) * lda < (1L << 30), "gemm: activation above 2 GiB (32-bit byte offsets)");
-  // plain GEMMs of the shapes measured faster on hipBLASLt go there (one group, no epilogue,
-  // BF16 output, no forced tile); it declines, and the kernels below run, when it cannot launch
-  if (groups == 1 && epilogue == IRIS_EPI_NONE && c_dtype == IRIS_BF16 && g_forced_tile < 0 && m[0] > 0 &&
-      blaslt_wanted(m[0], n, k) &&
-      blaslt_linear(static_cast<const bf16*>(a[0]), static_cast<const bf16*>(b[0]), bias ? bias[0] : nullptr,
-                    static_cast<bf16*>(c[0]), m[0], n, k, lda, ldb, ldc, stream))
-    return check_launch("gemm (hipBLASLt)");
   const SplitPlan plan = plan_split(m, groups, n, epilogue, g_forced_tile);
   if (plan.n1 == 0)
     return gemm_part(groups, a, b, bias, c, m, c_dtype, n, k, lda, ldb, ldc, epilogue,

@@ -34,15 +34,6 @@ from .config import ModelConfig
 HEAD_DIM = K.HEAD_DIM
 
 
-def _per_image_linear(x: torch.Tensor, weight: torch.Tensor, bias, out: torch.Tensor, rows: int) -> None:
-    """``K.linear`` one batch item (``rows`` rows) at a time. These are the plain GEMMs the
-    library runs on hipBLASLt, whose algorithm and summation order follow the problem's row
-    count; one call per item keeps every row's result independent of the batch (the library's
-    own kernels are row-independent at any size)."""
-    for r in range(0, x.shape[0], rows):
-        K.linear(x[r:r + rows], weight, bias, out=out[r:r + rows])
-
-
 def check_supported(cfg: ModelConfig) -> None:
     """Reject topologies the fused forward does not handle (src/iris_metal/model.py:68-93)."""
     requirements = {
@@ -578,7 +569,7 @@ class HipIris:
         K.gated_residual_norm_modulate_(Rv, branch.view(B, per_batch, D), blk["attn_post_norm"], m[2], eps,
                                         blk["norm2"], m[3], m[4], h2.view(B, per_batch, D))
         K.linear(h2, blk["w13"], out=hh, swiglu=True)
-        _per_image_linear(hh, blk["w2"], None, branch, per_batch)
+        K.linear(hh, blk["w2"], out=branch)
         if nxt is None:
             K.gated_residual_rms_norm_(Rv, branch.view(B, per_batch, D), blk["mlp_post_norm"], m[5], eps)
         else:
@@ -591,16 +582,16 @@ class HipIris:
         px = cfg.pixel
         heads = px.num_heads
         width = px.attn_hidden_size
-        _per_image_linear(ws["scond"], blk["adaln_w"], blk["adaln_b"], ws["mods_pix"].view(B * Lp, -1), Lp)
-        _per_image_linear(ws["hpix"].view(B * Lp, -1), blk["compress_w"], blk["compress_b"], ws["cp"], Lp)
-        _per_image_linear(ws["cp"], blk["qkv_w"], None, ws["pq"], Lp)
+        K.linear(ws["scond"], blk["adaln_w"], blk["adaln_b"], out=ws["mods_pix"].view(B * Lp, -1))
+        K.linear(ws["hpix"].view(B * Lp, -1), blk["compress_w"], blk["compress_b"], out=ws["cp"])
+        K.linear(ws["cp"], blk["qkv_w"], out=ws["pq"])
         rope_c, rope_s = ws["rope_pix"]
         pv = ws["pq"].view(B, Lp, 3 * width)
         K.qkv_prepare(pv, blk["q_norm"], blk["k_norm"], rope_c, rope_s, eps, heads, heads, ws["qp"], ws["kp"],
                       ws["vtp"], 0, width, 2 * width)
         K.flash_attention(ws["qp"], ws["kp"], ws["vtp"], Lp, None, ws["pa"], n_split=0)
-        _per_image_linear(ws["pa"], blk["proj_w"], blk["proj_b"], ws["pr"], Lp)
-        _per_image_linear(ws["pr"], blk["expand_w"], blk["expand_b"], ws["ex"], Lp)
+        K.linear(ws["pa"], blk["proj_w"], blk["proj_b"], out=ws["pr"])
+        K.linear(ws["pr"], blk["expand_w"], blk["expand_b"], out=ws["ex"])
         K.pixel_mlp_(ws["pixels"], ws["ex"].view_as(ws["hpix"]), ws["mods_pix"], blk["norm2"],
                      (blk["fc1_w"], blk["fc1_b"]), (blk["fc2_w"], blk["fc2_b"]), next_norm, eps,
                      next_input=ws["hpix"])
@@ -736,7 +727,7 @@ class HipIris:
             K.linear(att, blk["proj_w"], blk["proj_b"], out=br)
             K.residual_rms_norm(Y, br, blk["norm2"], eps, hy)
             K.linear(hy, blk["w13"], out=hh, swiglu=True)
-            _per_image_linear(hh, blk["w2"], None, br, n)
+            K.linear(hh, blk["w2"], out=br)
             if i + 1 < len(self.text_blocks):
                 K.residual_rms_norm(Y, br, self.text_blocks[i + 1]["norm1"], eps, hy)
             else:

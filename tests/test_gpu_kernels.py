@@ -395,44 +395,48 @@ def test_gemm_bf16_output_over_several_rounds(tile, shape, swiglu):
     close_bf16(out[rows], want)
 
 
-@pytest.mark.parametrize("nk,bias", [((2560, 6848), False), ((16384, 2560), True), ((1280, 4096), True),
-                                     ((3840, 1280), False), ((1280, 1280), True), ((4096, 1280), True)])
-def test_gemm_hipblaslt_shapes_eager_and_graph_replays(nk, bias):
-    """The plain GEMMs routed to hipBLASLt (BF16 output, optional FP32 bias): against an FP32
-    product on sampled rows, the same as the library's own four-wave kernel to BF16 rounding,
-    and bit for bit the same when recorded in a HIP graph and replayed several times with eager
-    work and synchronisation between the replays."""
-    n, k = nk
-    m = 4352 if n == 2560 else 4096
+@pytest.mark.parametrize("rows,n,k,bias", [((4352,), 2560, 6848, False), ((4096, 256), 2560, 6848, False),
+                                            ((4096,), 16384, 2560, True), ((4096,), 1280, 4096, True),
+                                            ((4096,), 3840, 1280, False), ((4096,), 1280, 1280, True),
+                                            ((4096,), 4096, 1280, True), ((17408,), 2560, 6848, False)])
+def test_gemm_plain_step_shapes_eager_and_graph_replays(rows, n, k, bias):
+    """The step's plain GEMMs (BF16 output, optional FP32 bias): the single-stream w2, the dual
+    blocks' grouped image + text w2, the pixel stage's adaLN, compress, q|k|v, proj and expand,
+    and a guided batch of four images' w2. Against an FP32 product on sampled rows; every row
+    bit for bit the same as the same rows computed alone (the summation order does not depend on
+    the row count or the tile); and bit for bit the same when recorded in a HIP graph and replayed
+    several times with eager work and synchronisation between the replays."""
     g = torch.Generator(device=DEV).manual_seed(41)
-    a = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
-    w = (0.02 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16)
-    b = torch.randn(n, generator=g, device=DEV) if bias else None
-    eager = K.linear(a, w, b)
-    _lib.call("iris_gemm_force_tile", 11 if n >= 2560 else 12)
-    try:
-        own = K.linear(a, w, b)
-    finally:
-        _lib.call("iris_gemm_force_tile", -1)
-    rows = torch.cat([torch.arange(0, m, 53), torch.tensor([m - 1])])
-    want = _gemm_ref(a[rows], w, b)
-    close_bf16(eager[rows], want)
-    close_bf16(eager[rows], own[rows].float())
-    out = torch.empty_like(eager)
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        K.linear(a, w, b, out=out)  # the problem's set-up happens outside the capture
-    torch.cuda.current_stream().wait_stream(stream)
+    xs = [torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16) for m in rows]
+    ws = [(0.02 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16) for _ in rows]
+    bs = [torch.randn(n, generator=g, device=DEV) for _ in rows] if bias else None
+
+    def run(outs=None):
+        outs = outs or [torch.empty(m, n, device=DEV, dtype=torch.bfloat16) for m in rows]
+        if len(rows) == 1:
+            K.linear(xs[0], ws[0], bs[0] if bias else None, out=outs[0])
+        else:
+            K.linear_grouped(xs, ws, bs, outs)
+        return outs
+
+    got = run()
+    for i, m in enumerate(rows):
+        sel = torch.cat([torch.arange(0, m, 37), torch.tensor([m - 1])])
+        want = _gemm_ref(xs[i][sel].cpu(), ws[i].cpu(), bs[i].cpu() if bias else None)
+        close_bf16(got[i][sel], want)
+        part = K.linear(xs[i][:300].contiguous(), ws[i], bs[i] if bias else None)
+        assert torch.equal(part, got[i][:300])
+    outs = [torch.empty_like(o) for o in got]
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        K.linear(a, w, b, out=out)
-    for _ in range(4):
-        out.fill_(7.0)
+        run(outs)
+    for _ in range(3):
+        for o in outs:
+            o.fill_(7.0)
         graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(out, eager)
-        K.linear(a[:64], w, b)  # eager work between the replays
+        assert all(torch.equal(o, e) for o, e in zip(outs, got))
+        run()  # eager work between the replays
         torch.cuda.synchronize()
 
 
