@@ -236,9 +236,12 @@ int iris_pixel_rms_norm(const void* pixels, int pixels_dtype, void* out, const f
                         float eps, hipStream_t stream);
 
 /* pixel_mlp_ (src/iris_metal/kernels.py:235-293, wrapper 527-584), per pixel of 16 channels:
- * x = pixels + branch*(1+scale1)+shift1; h = rmsnorm(x)*norm_weight;
- * x += (fc2(gelu_erf(fc1(h))))*(1+scale2)+shift2; pixels = x; next_input = rmsnorm(x)*next_norm_weight.
- * mods BF16 [n_pixels, 64] = (scale1, shift1, scale2, shift2); fc1 [64,16], fc2 [16,64] FP32. */
+ * x = pixels + branch*(1+scale1)+shift1; h = bf16(rmsnorm(x)*norm_weight);
+ * a = bf16(fc1(h)); g = bf16(gelu(a)) (exact-erf GELU, correctly rounded);
+ * x += fc2(g)*(1+scale2)+shift2; pixels = x; next_input = rmsnorm(x)*next_norm_weight.
+ * The BF16 points (h, a, g and both weights) are the reference kernel's; fc1 / fc2 run on BF16 MFMA
+ * with FP32 sums, the stream and the modulation stay FP32 (pixels_dtype F32) or round on store (BF16).
+ * mods BF16 [n_pixels, 64] = (scale1, shift1, scale2, shift2); fc1 [64,16], fc2 [16,64] FP32 in memory. */
 int iris_pixel_mlp(void* pixels, int pixels_dtype, const void* branch, const void* mods, const float* norm_weight,
                    const float* fc1_w, const float* fc1_b, const float* fc2_w, const float* fc2_b,
                    const float* next_norm_weight, void* next_input, long n_pixels, float eps, hipStream_t stream);

@@ -1,7 +1,10 @@
 // Pixel-stage bandwidth kernels: patchify + pixel embedding, the per-pixel RMSNorm, the
 // post-modulated PiT tail (norm, 16 -> 64 -> 16 exact-GELU MLP, both modulated residual
-// adds, next block's norm) and the 16 -> 3 head with unpatchify. One thread per pixel,
-// all math in FP32; BF16 only where the value is stored.
+// adds, next block's norm) and the 16 -> 3 head with unpatchify. One thread per pixel and
+// FP32 math (BF16 only where the value is stored), except the MLP's two products, which run
+// on BF16 MFMA at the reference's BF16 rounding points.
+#include <algorithm>
+
 #include "iris_common.hpp"
 
 namespace iris {
@@ -77,86 +80,191 @@ __global__ __launch_bounds__(256) void pixel_rms_norm_kernel(const TP* __restric
   store8(out + idx * kPix + 8, v + 8);
 }
 
-// Exact GELU a Phi(a), Phi(a) = erfc(-a / sqrt 2) / 2, with erfc(z), z >= 0, by the Chebyshev fit of
-// Press et al., Numerical Recipes in C (2nd ed.) sec. 6.2 ("erfcc", fractional error < 1.2e-7
-// everywhere): erfc(z) = t exp(-z^2 + P(t)), t = 1 / (1 + z / 2), P a degree-9 polynomial; and
-// Phi(a) = 1 - erfc(|a| / sqrt 2) / 2 for a >= 0. The tail a << 0 keeps full relative precision:
-// z^2 = a^2 / 2 is carried as hi + lo (exact square split by an fma, halved exactly), and
-// exp(-hi) is taken as exp2 of hi log2(e) with the product's rounding error moved into the
-// small second factor. About twenty VALU instructions instead of the library erfcf's fifty.
-__device__ __forceinline__ float gelu_erf(float a) {
-  constexpr float kLog2e = 1.44269504088896341f;
-  const float z = fabsf(a) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
-  float poly = 0.17087277f;
-  poly = fmaf(t, poly, -0.82215223f);
-  poly = fmaf(t, poly, 1.48851587f);
-  poly = fmaf(t, poly, -1.13520398f);
-  poly = fmaf(t, poly, 0.27886807f);
-  poly = fmaf(t, poly, -0.18628806f);
-  poly = fmaf(t, poly, 0.09678418f);
-  poly = fmaf(t, poly, 0.37409196f);
-  poly = fmaf(t, poly, 1.00002368f);
-  const float aa = a * a;
-  const float hi = 0.5f * aa;                      // z^2 = hi + lo
-  const float lo = 0.5f * fmaf(a, a, -aa);
-  const float small = fmaf(t, poly, -1.26551223f) - lo;
-  const float p = hi * kLog2e;
-  const float p_err = fmaf(hi, kLog2e, -p);        // hi log2(e) = p + p_err
-  const float q = (0.5f * t) * __builtin_amdgcn_exp2f(-p) * __builtin_amdgcn_exp2f(fmaf(small, kLog2e, -p_err));
-  return a * (a >= 0.0f ? 1.0f - q : q);
+#include "gelu_bf16_table.inc"
+
+constexpr unsigned kGeluLo = kGeluLowExponent << 7;  // |bits| of the first table argument
+constexpr unsigned kGeluN = kGeluPerSign;
+
+// GELU of a pre-activation rounded to BF16, itself rounded to BF16 (the pixel MLP's two
+// rounding points, src/iris_metal/kernels.py:273-274), from the correctly rounded table of the
+// BF16 arguments 2^-16 <= |a| < 256 held in LDS. Below that range a Phi(a) lies within half an
+// ulp of a / 2, above it GELU(a) is a (a > 0) or underflows to 0; all three cases agree with
+// the correctly rounded exact-erf GELU for every finite BF16 argument. A NaN passes through,
+// -inf gives 0.
+__device__ __forceinline__ bf16 gelu_bf16(float a, const unsigned short* tab) {
+  const bf16 ab = static_cast<bf16>(a);
+  const unsigned u = __builtin_bit_cast(unsigned short, ab);
+  const unsigned t = (u & 0x7fffu) - kGeluLo;  // wraps for |a| < 2^-16
+  const unsigned short tv = tab[min(t, kGeluN - 1) + (u >> 15) * kGeluN];
+  const float af = static_cast<float>(ab);
+  const float outside = static_cast<int>(t) < 0 ? 0.5f * af : (af <= 0.0f ? 0.0f : af);
+  return t < kGeluN ? __builtin_bit_cast(bf16, tv) : static_cast<bf16>(outside);
 }
 
+// The table-only GELU of two pre-activations, packed as a BF16 pair; `worst` collects the
+// largest table offset seen (an offset >= kGeluN marks an argument outside the table, whose
+// entry here is a clamped stand-in that the caller must replace).
+__device__ __forceinline__ unsigned gelu2_table(float a0, float a1, const unsigned short* tab, unsigned& worst) {
+  const unsigned pk = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{a0, a1}, bf16x2));
+  const unsigned t0 = (pk & 0x7fffu) - kGeluLo;
+  const unsigned t1 = ((pk >> 16) & 0x7fffu) - kGeluLo;
+  worst = max(worst, max(t0, t1));
+  const unsigned v0 = tab[min(t0, kGeluN - 1) + ((pk >> 15) & 1u) * kGeluN];
+  const unsigned v1 = tab[min(t1, kGeluN - 1) + (pk >> 31) * kGeluN];
+  return v0 | (v1 << 16);
+}
+
+// Sum of a lane's value and its partner's (lane ^ 32); the same bits on both, as the sum commutes.
+__device__ __forceinline__ float pair_sum(float v) { return v + __shfl_xor(v, 32); }
+
+// One lane's share of a pixel as it comes from memory: 8 stream channels, 8 branch channels
+// and the 4 x 8 modulation values of those channels.
+template <typename TP>
+struct PixelShare {
+  TP x[8];
+  bf16x8 br, s1, t1, s2, t2;
+};
+
+template <typename TP>
+__device__ __forceinline__ void load_share(PixelShare<TP>& d, const TP* pixels, const bf16* branch, const bf16* mods,
+                                           long idx, int c0) {
+  if constexpr (sizeof(TP) == 4) {
+    *reinterpret_cast<f32x4*>(d.x) = *reinterpret_cast<const f32x4*>(pixels + idx * kPix + c0);
+    *reinterpret_cast<f32x4*>(d.x + 4) = *reinterpret_cast<const f32x4*>(pixels + idx * kPix + c0 + 4);
+  } else {
+    *reinterpret_cast<bf16x8*>(d.x) = *reinterpret_cast<const bf16x8*>(pixels + idx * kPix + c0);
+  }
+  d.br = *reinterpret_cast<const bf16x8*>(branch + idx * kPix + c0);
+  const bf16* m = mods + idx * 4 * kPix + c0;
+  d.s1 = *reinterpret_cast<const bf16x8*>(m);
+  d.t1 = *reinterpret_cast<const bf16x8*>(m + kPix);
+  d.s2 = *reinterpret_cast<const bf16x8*>(m + 2 * kPix);
+  d.t2 = *reinterpret_cast<const bf16x8*>(m + 3 * kPix);
+}
+
+// The PiT tail on BF16 MFMA. A wave takes 32 pixels per step; lane l owns pixel l % 32 and
+// channels 8 (l / 32) .. 8 (l / 32) + 7, which is both the B-operand layout of
+// v_mfma_f32_32x32x16_bf16 (column l % 32, k = 8 (l / 32) + m) and, for the 16 output rows
+// of the second product, the accumulator layout once the rows are put in channel order
+// chan(i) (bits 2 and 3 of the row index swapped). Per step:
+//   x += branch (1 + scale1) + shift1; h = bf16(rmsnorm(x) * norm_w)        (FP32, two lanes)
+//   A^T[64 hidden, 32 px] = W1 h^T + b1                                      (2 MFMAs, K = 16)
+//   G = gelu_bf16(A^T), in place: the accumulator registers 8 jj .. 8 jj + 7 of hidden block
+//       blk are exactly a B operand over hidden units 32 blk + 16 jj + 8 (m / 4) + 4 (l / 32)
+//       + m % 4, and W2's columns are gathered in that order
+//   Y^T[16 ch, 32 px] = W2 G + b2                                            (4 MFMAs, K = 64)
+//   x += Y (1 + scale2) + shift2; pixels = x; next_input = bf16(rmsnorm(x) * next_w)
+// The weights (FP32 in memory) are rounded to BF16 as operands; sums accumulate in FP32. The
+// RMS sums add each lane's 8 squares in channel order and then the two halves. G comes from
+// the table alone unless some argument of the step lies outside it (|a| < 2^-16 or >= 256,
+// rare for O(1) activations): then the wave recomputes the step's G with the full rule. The
+// next step's inputs are loaded while the current one computes; lanes past the last pixel
+// load the last pixel and store nothing.
 template <typename TP>
 __global__ __launch_bounds__(256) void pixel_mlp_kernel(
     TP* __restrict__ pixels, const bf16* __restrict__ branch, const bf16* __restrict__ mods,
     const float* __restrict__ norm_w, const float* __restrict__ fc1_w, const float* __restrict__ fc1_b,
     const float* __restrict__ fc2_w, const float* __restrict__ fc2_b, const float* __restrict__ next_w,
-    bf16* __restrict__ next_input, long n_pixels, float eps) {
-  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= n_pixels) return;
-  float m[4 * kPix];
+    bf16* __restrict__ next_input, long n_pixels, long n_steps, float eps) {
+  __shared__ __align__(16) unsigned short tab[2 * kGeluN];
+  static_assert(2 * kGeluN * sizeof(unsigned short) % 16 == 0, "table copied in 16-byte pieces");
+  for (int i = threadIdx.x; i < static_cast<int>(2 * kGeluN / 8); i += 256)
+    reinterpret_cast<uint4*>(tab)[i] = reinterpret_cast<const uint4*>(kGeluBf16Table)[i];
+
+  const int lane = threadIdx.x & 63;
+  const int p = lane & 31, g = lane >> 5;
+  const int c0 = 8 * g;
+  bf16x8 w1[2], w2[4];
+  f32x16 b1[2], b2;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) load8(mods + idx * 4 * kPix + 8 * i, m + 8 * i);
-  float br[kPix], x[kPix];
-  load8(branch + idx * kPix, br);
-  load8(branch + idx * kPix + 8, br + 8);
-  load8(pixels + idx * kPix, x);
-  load8(pixels + idx * kPix + 8, x + 8);
-  float ss = 0.0f;
+  for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-  for (int c = 0; c < kPix; ++c) {
-    x[c] = x[c] + (br[c] * (1.0f + m[c]) + m[kPix + c]);  // scale1, shift1
-    ss += x[c] * x[c];
+    for (int m = 0; m < 8; ++m) w1[blk][m] = static_cast<bf16>(fc1_w[(32 * blk + p) * kPix + c0 + m]);
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) b1[blk][r] = fc1_b[32 * blk + 8 * (r >> 2) + 4 * g + (r & 3)];
+  // output row p < 16 holds channel ch; rows 16..31 are zero (their weights read row ch % 16)
+  const int ch = ((p >> 2) & 1) * 8 + ((p >> 3) & 1) * 4 + (p & 3);
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const float w = fc2_w[ch * kHidden + 16 * q + 8 * (m >> 2) + 4 * g + (m & 3)];
+      w2[q][m] = static_cast<bf16>(p < kPix ? w : 0.0f);
+    }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) b2[r] = r < 8 ? fc2_b[c0 + r] : 0.0f;
+  float nw[8], nnw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    nw[i] = norm_w[c0 + i];
+    nnw[i] = next_w[c0 + i];
   }
-  float r = rsqrtf(ss / kPix + eps);
-  float h[kPix], out[kPix];
+
+  const long n_waves = static_cast<long>(gridDim.x) * 4;
+  long step = static_cast<long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  PixelShare<TP> nxt;
+  if (step < n_steps) load_share(nxt, pixels, branch, mods, min(step * 32 + p, n_pixels - 1), c0);
+  __syncthreads();
+
+  for (; step < n_steps; step += n_waves) {
+    const PixelShare<TP> cur = nxt;
+    if (step + n_waves < n_steps)
+      load_share(nxt, pixels, branch, mods, min((step + n_waves) * 32 + p, n_pixels - 1), c0);
+    const long idx = step * 32 + p;
+    float x[8];
+    float ss = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kPix; ++c) {
-    h[c] = (x[c] * r) * norm_w[c];
-    out[c] = fc2_b[c];
+    for (int i = 0; i < 8; ++i) {
+      x[i] = to_f32(cur.x[i]) + (to_f32(cur.br[i]) * (1.0f + to_f32(cur.s1[i])) + to_f32(cur.t1[i]));
+      ss += x[i] * x[i];
+    }
+    float r = rsqrtf(pair_sum(ss) / kPix + eps);
+    bf16x8 hb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hb[i] = static_cast<bf16>((x[i] * r) * nw[i]);
+    f32x16 acc[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) acc[blk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1[blk], hb, b1[blk], 0, 0, 0);
+    unsigned worst = 0;
+    f32x16 y = b2;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint4 gb;
+      const f32x16& a = acc[q >> 1];
+      const int o = 8 * (q & 1);
+      gb.x = gelu2_table(a[o + 0], a[o + 1], tab, worst);
+      gb.y = gelu2_table(a[o + 2], a[o + 3], tab, worst);
+      gb.z = gelu2_table(a[o + 4], a[o + 5], tab, worst);
+      gb.w = gelu2_table(a[o + 6], a[o + 7], tab, worst);
+      y = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w2[q], __builtin_bit_cast(bf16x8, gb), y, 0, 0, 0);
+    }
+    if (__builtin_expect(__any(worst >= kGeluN), 0)) {  // wave-uniform
+      y = b2;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        bf16x8 gx;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) gx[m] = gelu_bf16(acc[q >> 1][8 * (q & 1) + m], tab);
+        y = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w2[q], gx, y, 0, 0, 0);
+      }
+    }
+    ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[i] = x[i] + (y[i] * (1.0f + to_f32(cur.s2[i])) + to_f32(cur.t2[i]));
+      ss += x[i] * x[i];
+    }
+    r = rsqrtf(pair_sum(ss) / kPix + eps);
+    if (idx < n_pixels) {
+      store8(pixels + idx * kPix + c0, x);
+      float hn[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hn[i] = (x[i] * r) * nnw[i];
+      store8(next_input + idx * kPix + c0, hn);
+    }
   }
-  for (int j = 0; j < kHidden; ++j) {
-    float a = fc1_b[j];
-#pragma unroll
-    for (int c = 0; c < kPix; ++c) a += fc1_w[j * kPix + c] * h[c];
-    const float g = gelu_erf(a);
-#pragma unroll
-    for (int c = 0; c < kPix; ++c) out[c] += fc2_w[c * kHidden + j] * g;
-  }
-  ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < kPix; ++c) {
-    x[c] = x[c] + (out[c] * (1.0f + m[2 * kPix + c]) + m[3 * kPix + c]);  // scale2, shift2
-    ss += x[c] * x[c];
-  }
-  store8(pixels + idx * kPix, x);
-  store8(pixels + idx * kPix + 8, x + 8);
-  r = rsqrtf(ss / kPix + eps);
-#pragma unroll
-  for (int c = 0; c < kPix; ++c) h[c] = (x[c] * r) * next_w[c];
-  store8(next_input + idx * kPix, h);
-  store8(next_input + idx * kPix + 8, h + 8);
 }
 
 // CO output channels: 3 (the predicted flow) or 1 (the depth head with its 1x1 reducer folded in).
@@ -258,14 +366,18 @@ extern "C" int iris_pixel_mlp(void* pixels, int pixels_dtype, const void* branch
                    next_input,
                "pixel_mlp_: null pointer");
   if (n_pixels == 0) return IRIS_OK;
+  // 32 pixels per wave step, 4 waves per workgroup, at most 4 workgroups per CU (each copies
+  // the 12 KB GELU table into its LDS once)
+  const long n_steps = (n_pixels + 31) / 32;
+  const unsigned blocks = static_cast<unsigned>(std::min<long>((n_steps + 3) / 4, 4L * device_cus()));
   if (pixels_dtype == IRIS_F32)
-    pixel_mlp_kernel<float><<<blocks_for(n_pixels), 256, 0, stream>>>(
+    pixel_mlp_kernel<float><<<blocks, 256, 0, stream>>>(
         (float*)pixels, (const bf16*)branch, (const bf16*)mods, norm_weight, fc1_w, fc1_b, fc2_w, fc2_b,
-        next_norm_weight, (bf16*)next_input, n_pixels, eps);
+        next_norm_weight, (bf16*)next_input, n_pixels, n_steps, eps);
   else
-    pixel_mlp_kernel<bf16><<<blocks_for(n_pixels), 256, 0, stream>>>(
+    pixel_mlp_kernel<bf16><<<blocks, 256, 0, stream>>>(
         (bf16*)pixels, (const bf16*)branch, (const bf16*)mods, norm_weight, fc1_w, fc1_b, fc2_w, fc2_b,
-        next_norm_weight, (bf16*)next_input, n_pixels, eps);
+        next_norm_weight, (bf16*)next_input, n_pixels, n_steps, eps);
   return check_launch("pixel_mlp");
 }
 

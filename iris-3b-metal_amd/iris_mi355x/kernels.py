@@ -269,7 +269,10 @@ def pixel_mlp_(
     """Finish a post-modulated PiT block in place; return the next block's normed input
     (src/iris_metal/kernels.py:527-584). ``pixels``: FP32 or BF16 ``[..., 16]`` (updated in
     place); ``branch``: BF16 ``[..., 16]``; ``mods``: BF16 ``[..., 64]`` (scale1, shift1,
-    scale2, shift2); ``fc1``/``fc2``: ``nn.Linear`` (or ``(weight, bias)``) of 16 -> 64 -> 16."""
+    scale2, shift2); ``fc1``/``fc2``: ``nn.Linear`` (or ``(weight, bias)``) of 16 -> 64 -> 16.
+    The MLP rounds where the reference kernel does (src/iris_metal/kernels.py:268-280): the normed
+    input, both weights, the pre-activation and the exact-erf GELU (correctly rounded) are BF16,
+    the two products BF16 MFMA with FP32 sums; the stream and both modulations stay FP32."""
     check = _Check("pixel_mlp_", pixels, branch, mods, norm_weight, next_norm_weight)
     w1, b1 = _linear_params(fc1)
     w2, b2 = _linear_params(fc2)

@@ -8,6 +8,7 @@ import math
 import pytest
 import torch
 import torch.nn.functional as F
+from scipy.special import ndtr
 
 from iris_mi355x import _lib
 from iris_mi355x import kernels as K
@@ -886,7 +887,38 @@ def test_patchify_embed_and_head(hw, patch, channels, out_channels):
     torch.testing.assert_close(out.cpu(), want, rtol=1e-5, atol=1e-5)
 
 
+def _bf16(t):
+    return t.to(torch.bfloat16).float()
+
+
+def _gelu_exact(a):
+    """a Phi(a) in float64 with scipy's ndtr for Phi, which keeps full relative precision for
+    a << 0 (torch's float64 ndtr cancels below a ~ -7.5)."""
+    a = a.double()
+    return a * torch.from_numpy(ndtr(a.numpy()))
+
+
+def _pixel_mlp_at_bf16_points(pixels, branch, mods, nw, fc1, fc2, nnw, eps):
+    """The PiT tail at the kernel's BF16 rounding points, which are the reference's
+    (src/iris_metal/kernels.py:256-287): h, both weights, the pre-activation and the GELU output
+    in BF16; products summed exactly (float64) and the stream in FP32."""
+    m = mods.float()
+    scale1, shift1, scale2, shift2 = m.chunk(4, dim=-1)
+    x = pixels + O.modulate(branch.float(), shift1, scale1)
+    h = _bf16(O.rms_norm(x, nw, eps))
+    a = _bf16((h.double() @ _bf16(fc1[0]).double().T + fc1[1].double()).float())
+    g = _bf16(_gelu_exact(a).float())
+    y = (g.double() @ _bf16(fc2[0]).double().T + fc2[1].double()).float()
+    x = x + O.modulate(y, shift2, scale2)
+    return x, g, m
+
+
 def test_pixel_mlp_matches_post_modulated_tail():
+    """In-place stream and next-block input against the tail at the BF16 rounding points, and
+    the MLP branch against the FP32 oracle. Where the kernel's FP32 sum of a pre-activation and
+    the exact one round to neighbouring BF16 values (a sum within an FP32 ulp or so of a BF16
+    midpoint, about one pre-activation in 10^5), that pixel moves by up to one BF16 step of one
+    GELU output times its fc2 weight: such pixels are bounded by that step and must be rare."""
     n = 4096 * 3 + 17
     g = gen(13)
     pixels = torch.randn(n, 16, generator=g)
@@ -895,23 +927,40 @@ def test_pixel_mlp_matches_post_modulated_tail():
     nw, nnw = 1 + 0.1 * torch.randn(16, generator=g), 1 + 0.1 * torch.randn(16, generator=g)
     fc1 = (0.3 * torch.randn(64, 16, generator=g), 0.1 * torch.randn(64, generator=g))
     fc2 = (0.3 * torch.randn(16, 64, generator=g), 0.1 * torch.randn(16, generator=g))
-    p = {"m.fc1.weight": fc1[0], "m.fc1.bias": fc1[1], "m.fc2.weight": fc2[0], "m.fc2.bias": fc2[1]}
-    m = mods.float()
-    scale1, shift1, scale2, shift2 = m.chunk(4, dim=-1)
-    x = pixels + O.modulate(branch.float(), shift1, scale1)
-    x = x + O.modulate(O.gelu_mlp(p, "m", O.rms_norm(x, nw, 1e-6)), shift2, scale2)
-    want_next = O.rms_norm(x, nnw, 1e-6)
+    want, gel, m = _pixel_mlp_at_bf16_points(pixels, branch, mods, nw, fc1, fc2, nnw, 1e-6)
     pd = pixels.to(DEV)
     nxt = K.pixel_mlp_(pd, branch.to(DEV), mods.to(DEV), nw.to(DEV), fc1, fc2, nnw.to(DEV), 1e-6)
-    torch.testing.assert_close(pd.cpu(), x, rtol=2e-5, atol=2e-5)
-    close_bf16(nxt, want_next)
+    got = pd.cpu()
+    err = (got - want).abs()
+    tight = 2e-5 + 2e-5 * want.abs()
+    flip = 2 * 2.0 ** -8 * gel.abs().max() * _bf16(fc2[0]).abs().max() * (1 + m[:, 32:48].abs().max())
+    print(f"pixel MLP: {int((err > tight).sum())} of {err.numel()} values beyond FP32 rounding, max err "
+          f"{err.max().item():.2e} (one-flip bound {flip.item():.2e})", flush=True)
+    assert (err > tight).float().mean().item() < 1e-3
+    assert torch.all(err <= tight + flip)
+    close_bf16(nxt, O.rms_norm(want, nnw, 1e-6), floor=2e-3)
+
+    # the MLP branch against the FP32 oracle: within the BF16 rounding of h, the weights and G
+    p = {"m.fc1.weight": fc1[0], "m.fc1.bias": fc1[1], "m.fc2.weight": fc2[0], "m.fc2.bias": fc2[1]}
+    scale1, shift1, scale2, shift2 = m.chunk(4, dim=-1)
+    x1 = pixels + O.modulate(branch.float(), shift1, scale1)
+    ref = O.modulate(O.gelu_mlp(p, "m", O.rms_norm(x1, nw, 1e-6)), shift2, scale2)
+    rel = ((got - x1) - ref).norm() / ref.norm()
+    assert rel.item() < 8e-3, rel.item()
 
 
-def test_pixel_mlp_gelu_is_exact_erf():
-    """The exact-erf GELU of the pixel MLP against torch's, over 4096 BF16 arguments in
-    [-8, 8] (a zero norm gain makes every hidden pre-activation equal its bias, and an identity
-    fc2 routes hidden units 0..15 to the 16 output channels of a zero pixel stream)."""
-    args = torch.linspace(-8, 8, 4096).to(torch.bfloat16).float()
+def test_pixel_mlp_gelu_is_correctly_rounded_erf():
+    """The GELU of the pixel MLP at every BF16 argument of its table (2^-10 <= |a| < 32) and at
+    arguments on both sides of it: the exact-erf GELU correctly rounded to BF16, checked as the
+    nearest BF16 to a Phi(a) in float64 (a zero norm gain makes every hidden pre-activation equal
+    its bias, and an identity fc2 routes hidden units 0..15 to the 16 output channels of a zero
+    pixel stream)."""
+    table_bits = torch.cat([torch.arange(117 << 7, 132 << 7), torch.arange(117 << 7, 132 << 7) | 0x8000])
+    edge = torch.tensor([0.0, -0.0, 2.0 ** -11, -(2.0 ** -11), 3.0 * 2.0 ** -12, 1e-30, -1e-30,
+                         2.0 ** -10 * 0.99, 31.9, -31.9, 32.0, -32.0, 100.0, -100.0, 1e30, -1e30, 7.0, -7.0,
+                         -5.5, -9.0, -13.0, -13.5, -14.0, 0.5, -0.5, 1.0, -1.0, 3.0, -3.0, 4.0])
+    args = torch.cat([table_bits.to(torch.int16).view(torch.bfloat16).float(), _bf16(edge)])
+    args = torch.cat([args, torch.zeros((-args.numel()) % 16)])
     zeros16 = torch.zeros(16, device=DEV)
     fc2 = (torch.eye(16, 64), torch.zeros(16))
     got = []
@@ -923,11 +972,22 @@ def test_pixel_mlp_gelu_is_exact_erf():
                      torch.zeros(64, 64, device=DEV, dtype=torch.bfloat16), zeros16,
                      (torch.zeros(64, 16), fc1_b), fc2, torch.ones(16, device=DEV), 1e-6)
         got.append(pixels[0].cpu())
-    got = torch.cat(got).double()
-    want = F.gelu(args.double())  # float64: the FP32 textbook formula itself cancels for a << 0
-    # relative to 4e-6 wherever |gelu| > ~1e-7; below that (a < -5.2) within 1e-12 absolute
-    torch.testing.assert_close(got, want, rtol=4e-6, atol=1e-12)
-    torch.testing.assert_close(got.float(), F.gelu(args), rtol=2e-6, atol=1e-6)
+    got = torch.cat(got)
+    assert torch.equal(got, _bf16(got)), "outputs are BF16 values"
+    exact = _gelu_exact(args)
+    bits = got.to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+    for step in (-1, 1):  # both BF16 neighbours (same sign) are no closer than the result
+        nb_bits = bits + step
+        nb = (nb_bits & 0xFFFF).to(torch.int16).view(torch.bfloat16).double()
+        valid = ((nb_bits & 0x7F80) != 0x7F80) & ((nb_bits & 0x8000) == (bits & 0x8000)) & (got != 0)
+        closer = (nb - exact).abs() < (got.double() - exact).abs()
+        assert not torch.any(closer & valid), args[closer & valid][:8]
+    # zero results only where a Phi(a) is below half the smallest BF16 subnormal
+    zero = got == 0
+    assert torch.all(exact[zero].abs() <= 2.0 ** -134), args[zero & (exact.abs() > 2.0 ** -134)]
+    # the textbook FP32 formula a (1 + erf(a / sqrt 2)) / 2 agrees where it does not cancel (a > -3)
+    ok = args > -3
+    close_bf16(got[ok], F.gelu(args[ok]), floor=0.0)
 
 
 def test_flow_euler_is_bitwise_the_reference_update():
