@@ -26,7 +26,8 @@ Prints one JSON line. Besides the driver's fields it carries:
   and ``cpu_turbo_4step_s`` beside it (the CPU sample's own wall time; with
   ``--cpu-step-only`` four times the timed step, marked as not measured);
 - ``fused_ops``: the row kernels' bandwidth microbenchmark at [1, 4352, 2560] BF16 (achieved
-  GB/s on algorithmic bytes, buffers rotated past the Infinity Cache);
+  GB/s on algorithmic bytes, buffers rotated past the Infinity Cache, calls back to back in a
+  replayed HIP graph as in the step; ``us_eager``: eager launches with their host gaps);
 - ``single_block``: one single-stream block at 1024x1024 (4352 joint tokens) on its own,
   algorithmic TFLOP over its HIP-event time against the BF16 peak;
 - ``guided``: 20 first-order guided steps (scale 3.0) over two prompts, a batch of four
@@ -452,7 +453,8 @@ def main() -> None:
 
         say("fused-op bandwidth microbenchmark")
         extras["fused_ops"] = {r["kernel"]: {"GB/s": r["GB/s"], "hbm_frac": r["hbm_frac"], "us": r["us"],
-                                             "bytes": r["bytes"]} for r in microbench.fused_ops()}
+                                             "us_eager": r["us_eager"], "bytes": r["bytes"]}
+                               for r in microbench.fused_ops()}
         say("single-stream block at 1024x1024")
         extras["single_block"] = single_block_leg(engine, cfg, text, dev)
         say("guided sampling, 20 steps, batch 4")
