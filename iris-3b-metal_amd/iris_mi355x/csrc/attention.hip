@@ -25,6 +25,8 @@
 // c ^ swz(r) so the 16-lane phases of ds_read_b128 hit 64 distinct banks.
 #include "iris_common.hpp"
 
+#include <utility>
+
 namespace iris {
 namespace {
 
@@ -91,6 +93,16 @@ __device__ __forceinline__ void store_row(const AttnArgs& p, const f32x16 (&o)[4
       store4(orow_ptr + d0, v);
     }
   }
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}) in order.
+template <int N, typename F, int... I>
+__device__ __forceinline__ void unroll_stages_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll_stages(F&& f) {
+  unroll_stages_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
 // STAGED: K/V tiles travel global -> registers (16-byte buffer loads) -> LDS (ds_write_b128)
@@ -219,11 +231,35 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
     for (int s = 0; s < STAGES - 1; ++s)
       if (s < n_tiles) issue(s, s);
   }
-  for (int t = 0; t < n_tiles; ++t) {
+  // Tile t uses stage S = t % STAGES, a compile-time constant in each copy of the body (the loop
+  // is unrolled by STAGES): the stage's LDS offsets become instruction immediates, so neither the
+  // fragment addresses nor the ring's M0 bases cost per-tile VALU / SALU work.
+  // Per-lane LDS element offsets of the fragment reads, the same in every tile and stage (the
+  // swizzle of a row depends on the lane's row within its 32-row block only): K step st of key
+  // block kb at kb * 32 * 128 + k_rd[st], V^T (kb, jj) of dim block db at db * 32 * KVT +
+  // v_rd[kb][jj]. Each tile re-declares them opaque to the compiler (an empty asm), so the
+  // stage and block constants fold into the reads' immediate offsets instead of becoming one
+  // hoisted address register per stage.
+  int k_rd[8], v_rd[KB][2];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) k_rd[st] = l32 * kHd + 8 * ((2 * st + g) ^ swz<16>(l32));
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) v_rd[kb][jj] = l32 * KVT + 8 * ((4 * kb + 2 * jj + g) ^ swz<VCPR>(l32));
+
+  auto tile = [&](const int t, auto stage) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage)::value;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) asm volatile("" : "+v"(k_rd[st]));
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) asm volatile("" : "+v"(v_rd[kb][jj]));
     if constexpr (STAGED) {
       // tile t + 1 (loaded during tile t - 1) into the stage tile t - 1 used, then load tile
       // t + 2; past the end both repeat the last tile into a stage nothing reads again
-      lwrite((t + 1) & 1);
+      lwrite((S + 1) & 1);
       gload(min(t + 2, n_tiles - 1));
     } else {
       if (t + STAGES - 2 < n_tiles)
@@ -231,9 +267,9 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
       else
         wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();  // tile t visible; stage (t-1) % STAGES no longer read
-      if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+      if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (S + STAGES - 1) % STAGES);
     }
-    const bf16* kl = lds + (t % STAGES) * STAGE;
+    const bf16* kl = lds + S * STAGE;
     const bf16* vl = kl + TILE;
 
     // S^T[key, q] for keys kb*32 + (8 (r/4) + 4 g + r%4), queries qb*32 + l32
@@ -248,10 +284,8 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
     bf16x8 kf[KD][KB];
     auto read_k = [&](int st, int slot) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const int r = kb * 32 + l32;
-        kf[slot][kb] = *reinterpret_cast<const bf16x8*>(kl + r * kHd + 8 * ((2 * st + g) ^ swz<16>(r)));
-      }
+      for (int kb = 0; kb < KB; ++kb)
+        kf[slot][kb] = *reinterpret_cast<const bf16x8*>(kl + kb * 32 * kHd + k_rd[st]);
     };
     // The S MFMAs issue at a raised wave priority: a wave in its MFMA phase is picked before the
     // waves of its SIMD that are in their softmax, which fill the gaps between its MFMAs
@@ -376,9 +410,7 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
     bf16x8 vfr[VD];
     auto read_v = [&](int i, int slot) {
       const int kb = i / 8, jj = (i / 4) % 2, db = i % 4;
-      const int c = 4 * kb + 2 * jj + g;
-      const int d = db * 32 + l32;
-      vfr[slot] = *reinterpret_cast<const bf16x8*>(vl + d * KVT + 8 * (c ^ swz<VCPR>(d)));
+      vfr[slot] = *reinterpret_cast<const bf16x8*>(vl + db * 32 * KVT + v_rd[kb][jj]);
     };
 #pragma unroll
     for (int i = 0; i < VD; ++i) read_v(i, i);
@@ -401,7 +433,16 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): tile t + 1 written, tile t's reads done
       __builtin_amdgcn_s_barrier();
     }
-  }
+  };
+  int t0 = 0;
+  for (; t0 + STAGES <= n_tiles; t0 += STAGES)
+    unroll_stages<STAGES>([&](auto stage) {
+      tile(t0 + decltype(stage)::value, stage);
+      __builtin_amdgcn_sched_barrier(0);  // each tile's registers are dead before the next one
+    });
+  unroll_stages<STAGES - 1>([&](auto stage) {
+    if (t0 + decltype(stage)::value < n_tiles) tile(t0 + decltype(stage)::value, stage);
+  });
   if constexpr (STAGED) wait_vmcnt<0>();  // the repeated loads past the last tile
 
   // epilogue: lane owns query q0 + qb*32 + l32
