@@ -234,19 +234,19 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
   // Tile t uses stage S = t % STAGES, a compile-time constant in each copy of the body (the loop
   // is unrolled by STAGES): the stage's LDS offsets become instruction immediates, so neither the
   // fragment addresses nor the ring's M0 bases cost per-tile VALU / SALU work.
-  // Per-lane LDS element offsets of the fragment reads, the same in every tile and stage (the
+  // Per-lane LDS byte offsets of the fragment reads, the same in every tile and stage (the
   // swizzle of a row depends on the lane's row within its 32-row block only): K step st of key
-  // block kb at kb * 32 * 128 + k_rd[st], V^T (kb, jj) of dim block db at db * 32 * KVT +
-  // v_rd[kb][jj]. Each tile re-declares them opaque to the compiler (an empty asm), so the
+  // block kb at kb * 32 * 256 + k_rd[st] bytes, V^T (kb, jj) of dim block db at db * 32 * 2 KVT
+  // + v_rd[kb][jj]. Each tile re-declares them opaque to the compiler (an empty asm), so the
   // stage and block constants fold into the reads' immediate offsets instead of becoming one
   // hoisted address register per stage.
   int k_rd[8], v_rd[KB][2];
 #pragma unroll
-  for (int st = 0; st < 8; ++st) k_rd[st] = l32 * kHd + 8 * ((2 * st + g) ^ swz<16>(l32));
+  for (int st = 0; st < 8; ++st) k_rd[st] = 2 * (l32 * kHd + 8 * ((2 * st + g) ^ swz<16>(l32)));
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) v_rd[kb][jj] = l32 * KVT + 8 * ((4 * kb + 2 * jj + g) ^ swz<VCPR>(l32));
+    for (int jj = 0; jj < 2; ++jj) v_rd[kb][jj] = 2 * (l32 * KVT + 8 * ((4 * kb + 2 * jj + g) ^ swz<VCPR>(l32)));
 
   auto tile = [&](const int t, auto stage) __attribute__((always_inline)) {
     constexpr int S = decltype(stage)::value;
@@ -285,7 +285,7 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
     auto read_k = [&](int st, int slot) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
-        kf[slot][kb] = *reinterpret_cast<const bf16x8*>(kl + kb * 32 * kHd + k_rd[st]);
+        kf[slot][kb] = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(kl + kb * 32 * kHd) + k_rd[st]);
     };
     // The S MFMAs issue at a raised wave priority: a wave in its MFMA phase is picked before the
     // waves of its SIMD that are in their softmax, which fill the gaps between its MFMAs
@@ -410,7 +410,7 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
     bf16x8 vfr[VD];
     auto read_v = [&](int i, int slot) {
       const int kb = i / 8, jj = (i / 4) % 2, db = i % 4;
-      vfr[slot] = *reinterpret_cast<const bf16x8*>(vl + db * 32 * KVT + v_rd[kb][jj]);
+      vfr[slot] = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(vl + db * 32 * KVT) + v_rd[kb][jj]);
     };
 #pragma unroll
     for (int i = 0; i < VD; ++i) read_v(i, i);
