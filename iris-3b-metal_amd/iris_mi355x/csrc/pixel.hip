@@ -345,8 +345,8 @@ extern "C" int iris_pixel_rms_norm(const void* pixels, int pixels_dtype, void* o
                                    long n_pixels, float eps, hipStream_t stream) {
   IRIS_REQUIRE(pixels_dtype == IRIS_F32 || pixels_dtype == IRIS_BF16, "pixel_rms_norm: unknown dtype");
   IRIS_REQUIRE(n_pixels >= 0, "pixel_rms_norm: bad size");
+  if (n_pixels == 0) return IRIS_OK;  // (empty tensors may come with null data pointers)
   IRIS_REQUIRE(pixels && out && weight, "pixel_rms_norm: null pointer");
-  if (n_pixels == 0) return IRIS_OK;
   if (pixels_dtype == IRIS_F32)
     pixel_rms_norm_kernel<float><<<blocks_for(n_pixels), 256, 0, stream>>>((const float*)pixels, (bf16*)out, weight,
                                                                            n_pixels, eps);
@@ -362,10 +362,10 @@ extern "C" int iris_pixel_mlp(void* pixels, int pixels_dtype, const void* branch
                               float eps, hipStream_t stream) {
   IRIS_REQUIRE(pixels_dtype == IRIS_F32 || pixels_dtype == IRIS_BF16, "pixel_mlp_: unknown dtype");
   IRIS_REQUIRE(n_pixels >= 0, "pixel_mlp_: bad size");
+  if (n_pixels == 0) return IRIS_OK;  // (empty tensors may come with null data pointers)
   IRIS_REQUIRE(pixels && branch && mods && norm_weight && fc1_w && fc1_b && fc2_w && fc2_b && next_norm_weight &&
                    next_input,
                "pixel_mlp_: null pointer");
-  if (n_pixels == 0) return IRIS_OK;
   // 32 pixels per wave step, 4 waves per workgroup, at most 4 workgroups per CU (each copies
   // the 12 KB GELU table into its LDS once)
   const long n_steps = (n_pixels + 31) / 32;

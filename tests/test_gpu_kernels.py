@@ -949,8 +949,33 @@ def test_pixel_mlp_matches_post_modulated_tail():
     assert rel.item() < 8e-3, rel.item()
 
 
+def test_pixel_mlp_bf16_stream_and_ragged_counts():
+    """The BF16 pixel stream (the reference kernel's storage type) against the same tail at the
+    BF16 rounding points with the stream read from and rounded back to BF16, at pixel counts that
+    leave a partial 32-pixel wave step (1, 31, 33, 100) and none (0): lanes past the last pixel
+    store nothing, and the pixels after the range stay untouched."""
+    g = gen(21)
+    fc1 = (0.3 * torch.randn(64, 16, generator=g), 0.1 * torch.randn(64, generator=g))
+    fc2 = (0.3 * torch.randn(16, 64, generator=g), 0.1 * torch.randn(16, generator=g))
+    nw, nnw = 1 + 0.1 * torch.randn(16, generator=g), 1 + 0.1 * torch.randn(16, generator=g)
+    for n in (0, 1, 31, 33, 100):
+        pixels = torch.randn(n + 7, 16, generator=g).to(torch.bfloat16)
+        branch = torch.randn(n, 16, generator=g).to(torch.bfloat16)
+        mods = (0.3 * torch.randn(n, 64, generator=g)).to(torch.bfloat16)
+        pd = pixels.to(DEV)
+        nxt = K.pixel_mlp_(pd[:n], branch.to(DEV), mods.to(DEV), nw.to(DEV), fc1, fc2, nnw.to(DEV), 1e-6)
+        got = pd.cpu()
+        assert torch.equal(got[n:], pixels[n:]), "pixels past the range were written"
+        if n == 0:
+            assert nxt.numel() == 0
+            continue
+        want, _, _ = _pixel_mlp_at_bf16_points(pixels[:n].float(), branch, mods, nw, fc1, fc2, nnw, 1e-6)
+        close_bf16(got[:n], want, floor=2e-3)
+        close_bf16(nxt, O.rms_norm(got[:n].float(), nnw, 1e-6), floor=2e-3)
+
+
 def test_pixel_mlp_gelu_is_correctly_rounded_erf():
-    """The GELU of the pixel MLP at every BF16 argument of its table (2^-10 <= |a| < 32) and at
+    """The GELU of the pixel MLP at every BF16 argument of its table (2^-16 <= |a| < 256) and at
     arguments on both sides of it: the exact-erf GELU correctly rounded to BF16, checked as the
     nearest BF16 to a Phi(a) in float64 (a zero norm gain makes every hidden pre-activation equal
     its bias, and an identity fc2 routes hidden units 0..15 to the 16 output channels of a zero
