@@ -783,6 +783,318 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
   }
 }
 
+// Epilogue of the 16 x 16 x 32 MFMA layout: acc[i][j][e] = C[m, n] with n = tile + wave col +
+// 16 i + 4 (lane / 16) + e, m = tile + wave row + 16 j + lane % 16. BF16 output is staged
+// through the LDS ring in rows padded by 16 bytes (a row of 160 outputs is 80 dwords, so
+// without the pad rows r and r + 4 would share banks) and leaves in 16-byte row chunks; FP32
+// output is stored straight from the registers. `mid` as in store_tile.
+template <int BM, int BN, int WM, int WN, int FM, int FN, int NW, int RING, typename TC, typename Mid>
+__device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, const TileJob& job, int N, long ldc,
+                                             int wm, int wn, Mid&& mid) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int M = job.m, tm = job.tm, tn = job.tn;
+  const float* __restrict__ bias = job.bias;
+  TC* __restrict__ C = static_cast<TC*>(job.c);
+  if constexpr (sizeof(TC) == 2) {
+    constexpr int PITCH = BN + 8;
+    static_assert(BM * PITCH <= RING, "output tile must fit in the LDS ring");
+    bf16* cl = lds;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      bf16* crow_l = cl + (wm * WM + 16 * j + l16) * PITCH;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const int nl = wn * WN + 16 * i + 4 * q4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
+        if (bias) {
+          const f32x4 bv = load4(bias + min(tn * BN + nl, N - 4));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += bv[e];
+        }
+        store_out4(crow_l + nl, v[0], v[1], v[2], v[3]);
+      }
+    }
+    __syncthreads();
+    mid();
+    constexpr int CHUNKS = BN / 8;
+    const int col0 = tn * BN;
+#pragma unroll 4
+    for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
+      const int r = idx / CHUNKS;
+      const int c = idx - r * CHUNKS;
+      const int m = tm * BM + r;
+      const int n0 = col0 + 8 * c;
+      if (m >= M || n0 >= N) continue;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * PITCH + 8 * c);
+      TC* dst = C + static_cast<long>(m) * ldc + n0;
+      if (n0 + 8 <= N) {
+        *reinterpret_cast<bf16x8*>(dst) = v;
+      } else {
+        *reinterpret_cast<bf16x4*>(dst) = bf16x4{v[0], v[1], v[2], v[3]};  // N % 4 == 0
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int m = tm * BM + wm * WM + 16 * j + l16;
+    if (m >= M) continue;
+    TC* crow = C + static_cast<long>(m) * ldc;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int n0 = tn * BN + wn * WN + 16 * i + 4 * q4;
+      if (n0 >= N) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
+      if (bias) {
+        const f32x4 bv = load4(bias + n0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += bv[e];
+      }
+      store_out4(crow + n0, v[0], v[1], v[2], v[3]);
+    }
+  }
+  mid();
+}
+
+// v_mfma_f32_16x16x32_bf16 accumulating in place, c += a b. Written as inline assembly: with the
+// builtin, the register allocator rotates the 40-odd four-register accumulator tuples of
+// gemm_w4h_kernel between registers inside the K loop (hundreds of accumulator moves per K
+// tile). An asm statement is also an ordering point for memory operations, so the LDS reads and
+// writes and the global loads between these MFMAs issue where the source places them. The
+// compiler pads no hazards for instructions it does not know to be MFMAs; the only ones it can
+// create are at the edges of straight-line MFMA runs, where it may zero or copy accumulators:
+// BEFORE pads a VALU write of an accumulator ahead of the run's first MFMA (5 wait states, more
+// than the 2 needed), AFTER pads a VALU read or write of the last MFMA's result behind it (24
+// wait states: 4 passes of 4 cycles plus the write-back). Inside a run every MFMA accumulates
+// into a tuple no other instruction touches, and a tuple's next MFMA is dozens of MFMAs later.
+template <bool BEFORE, bool AFTER>
+__device__ __forceinline__ void mfma16_acc(f32x4& c, const bf16x8& a, const bf16x8& b) {
+  // (the scheduling barriers keep the compiler from moving a VALU access of an accumulator
+  // into the run: asm statements order memory operations only)
+  if constexpr (BEFORE) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 4\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  } else if constexpr (AFTER) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 15\n\ts_nop 7" : "+a"(c) : "v"(a), "v"(b));
+    __builtin_amdgcn_sched_barrier(0);
+  } else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// Four waves (one per SIMD) in a 2 x 2 grid over a BM x BN tile on v_mfma_f32_16x16x32_bf16,
+// refilled as gemm_w4_kernel refills (K tile t + 2 loaded into registers while tile t is
+// multiplied, tile t + 1 written from them into the free LDS stage). The 16-row granularity
+// of this MFMA admits tiles the 32 x 32 one does not: 288 x 160 and 256 x 160 cut a 2560-column
+// output at 4352 and 4096 rows into 256 tiles (16 x 16; 192 x 256 tiles leave 26 of 256 CUs
+// idle there), 128 x 160 cuts 4096 x 1280 into 256. A K tile of 64 is two k-steps of 32. In
+// k-step 0 each of the first NR MFMAs is followed by one fragment read of k-step 1, the next
+// ones alternately by an LDS write of the first half of tile t + 1 and the load of tile t + 2
+// into the slot just written. In k-step 1 the second half follows the same way, then the wait
+// and barrier that publish tile t + 1 and retire stage t % 2, then one read of tile t + 1's
+// first fragments after each MFMA.
+template <int BM, int BN, int EPI, typename TC, bool PERSIST>
+__global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
+  constexpr int BK = 64, NW = 4;
+  constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+  constexpr int CPR = BK / 8;
+  constexpr int RPL = 64 / CPR;                // rows per 1 KB wave load
+  constexpr int A_LOADS = BM / RPL / NW;
+  constexpr int B_LOADS = BN / RPL / NW;
+  constexpr int LW = A_LOADS + B_LOADS;        // loads of 16 bytes per lane per K tile
+  constexpr int NR = FN + FM, NM = FN * FM;    // fragment reads and MFMAs per k-step
+  constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
+  static_assert(WM % 16 == 0 && WN % 16 == 0 && A_LOADS * RPL * NW == BM && B_LOADS * RPL * NW == BN,
+                "tile / wave split");
+  static_assert(EPI == IRIS_EPI_NONE, "plain or bias epilogue only");
+  constexpr int W0 = (LW + 1) / 2;             // slots written to LDS (and reloaded) in k-step 0
+  constexpr int W1 = LW - W0;                  // the rest, in k-step 1 before its barrier
+  static_assert(NR + 2 * W0 <= NM && 2 * W1 + NR < NM && W1 > 0, "MFMAs per k-step");
+  __shared__ __attribute__((aligned(1024))) bf16 lds[2 * STAGE];
+
+  int cur_tile = persistent_tile(p, 0);
+  if (cur_tile < 0) return;
+  TileJob job = locate_tile_at<BM, BN>(p, cur_tile);
+  const int N = p.n;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;
+
+  // load i: A rows (w A_LOADS + i) RPL .. + RPL for i < A_LOADS, B rows (w B_LOADS + i -
+  // A_LOADS) RPL .. for the rest; lane l fetches the chunk that belongs at byte 16 l of that
+  // 1 KB block in LDS. Byte offsets.
+  const int ld_r = lane / CPR;
+  const int ld_p = lane % CPR;
+  int off[LW];
+  auto set_offsets = [&](const TileJob& jb) {
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+      const bool is_a = i < A_LOADS;
+      const int r = (is_a ? w * A_LOADS + i : w * B_LOADS + i - A_LOADS) * RPL + ld_r;
+      off[i] = 2 * (is_a ? min(jb.tm * BM + r, jb.m - 1) * static_cast<int>(p.lda) + 8 * (ld_p ^ swz<BK>(r))
+                         : min(jb.tn * BN + r, N - 1) * static_cast<int>(p.ldb) + 8 * (ld_p ^ swz<BK>(r)));
+    }
+  };
+  set_offsets(job);
+  bf16x8 staged[LW];
+  __amdgpu_buffer_rsrc_t rsrc_a, rsrc_b;
+  auto set_rsrc = [&](const TileJob& jb) {
+    rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void*)jb.a, (short)0, jb.m * static_cast<int>(p.lda) * 2, kBufferFlags);
+    rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void*)jb.b, (short)0, N * static_cast<int>(p.ldb) * 2, kBufferFlags);
+  };
+  set_rsrc(job);
+  auto load1 = [&](int kt, int i) {
+    staged[i] =
+        __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(i < A_LOADS ? rsrc_a : rsrc_b, off[i], kt * BK * 2, 0));
+  };
+  auto write1 = [&](int stage, int i) {
+    bf16* blk = lds + stage * STAGE +
+                (i < A_LOADS ? (w * A_LOADS + i) * RPL * BK : A_STAGE + (w * B_LOADS + i - A_LOADS) * RPL * BK);
+    *reinterpret_cast<bf16x8*>(blk + 8 * lane) = staged[i];
+  };
+
+  // a 16-row fragment: lane l reads row l % 16 of the block, logical chunk 4 ks + l / 16 (the
+  // blocks start at multiples of 16 rows, so the swizzle depends on the lane only)
+  int frag_off[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) frag_off[ks] = l16 * BK + 8 * ((4 * ks + q4) ^ swz<BK>(l16));
+  bf16x8 wf[2][FN], xf[2][FM];
+  // read r of a k-step: weight fragment r (r < FN), else activation fragment r - FN
+  auto read1 = [&](int stage, int ks, int buf, int r) {
+    const bf16* s = lds + stage * STAGE + frag_off[ks];
+    if (r < FN)
+      wf[buf][r] = *reinterpret_cast<const bf16x8*>(s + A_STAGE + (wn * WN + 16 * r) * BK);
+    else
+      xf[buf][r - FN] = *reinterpret_cast<const bf16x8*>(s + (wm * WM + 16 * (r - FN)) * BK);
+  };
+  f32x4 acc[FN][FM];
+  auto zero_acc = [&] {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{};
+  };
+  zero_acc();
+  using T = std::true_type;
+  using F = std::false_type;
+  // MFMA idx of a k-step (row-major over the FN x FM tuples) from fragment buffer buf
+  auto mfma = [&](int buf, int idx, auto before, auto after) {
+    mfma16_acc<decltype(before)::value, decltype(after)::value>(acc[idx / FM][idx % FM], wf[buf][idx / FM],
+                                                                 xf[buf][idx % FM]);
+  };
+
+  // K tile t (t + 1 < KT) from stage S; FIRST / LAST: it opens / closes a straight-line run
+  auto ktile = [&](int t, auto S_, auto first_, auto last_) {
+    constexpr int S = decltype(S_)::value;
+    const int t2 = min(t + 2, p.k / BK - 1);
+#pragma unroll
+    for (int idx = 0; idx < NM; ++idx) {
+      if (idx == 0 && decltype(first_)::value)
+        mfma(0, idx, T{}, F{});
+      else
+        mfma(0, idx, F{}, F{});
+      if (idx < NR) {
+        read1(S, 1, 1, idx);
+      } else if (idx < NR + 2 * W0) {
+        const int q = (idx - NR) / 2;
+        if ((idx - NR) % 2 == 0)
+          write1(S ^ 1, q);
+        else
+          load1(t2, q);
+      }
+    }
+#pragma unroll
+    for (int idx = 0; idx < NM; ++idx) {
+      if (idx == NM - 1 && decltype(last_)::value)
+        mfma(1, idx, F{}, T{});
+      else
+        mfma(1, idx, F{}, F{});
+      if (idx < 2 * W1) {
+        const int q = W0 + idx / 2;
+        if (idx % 2 == 0) {
+          write1(S ^ 1, q);
+        } else {
+          load1(t2, q);
+          if (idx == 2 * W1 - 1) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes and reads are done
+            __builtin_amdgcn_s_barrier();
+          }
+        }
+      } else if (idx < 2 * W1 + NR) {
+        read1(S ^ 1, 0, 0, idx - 2 * W1);
+      }
+    }
+  };
+
+  const int KT = p.k / BK;
+#pragma unroll
+  for (int i = 0; i < LW; ++i) load1(0, i);
+  for (int round = 0;; ++round) {
+#pragma unroll
+  for (int i = 0; i < LW; ++i) write1(0, i);  // K tile 0, loaded before the previous tile's epilogue (or above)
+#pragma unroll
+  for (int i = 0; i < LW; ++i) load1(min(1, KT - 1), i);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read1(0, 0, 0, r);
+
+  int t = 0;
+  for (; t + 2 < KT; t += 2) {
+    ktile(t, std::integral_constant<int, 0>{}, T{}, F{});
+    ktile(t + 1, std::integral_constant<int, 1>{}, F{}, T{});
+  }
+  if (t + 1 < KT) {
+    ktile(t, std::integral_constant<int, 0>{}, T{}, T{});
+    ++t;
+  }
+  {  // last K tile, stage t % 2 (its k-step 1 fragments read between k-step 0's MFMAs)
+    const int S = t & 1;
+#pragma unroll
+    for (int idx = 0; idx < NM; ++idx) {
+      if (idx == 0)
+        mfma(0, idx, T{}, F{});
+      else
+        mfma(0, idx, F{}, F{});
+      if (idx < NR) read1(S, 1, 1, idx);
+    }
+#pragma unroll
+    for (int idx = 0; idx < NM; ++idx) {
+      if (idx == NM - 1)
+        mfma(1, idx, F{}, T{});
+      else
+        mfma(1, idx, F{}, F{});
+    }
+  }
+  wait_vmcnt<0>();  // the repeated loads of the last K tile
+  const int next_tile = PERSIST ? persistent_tile(p, round + 1) : -1;
+  const TileJob next = next_tile >= 0 ? locate_tile_at<BM, BN>(p, next_tile) : job;
+  store_tile16<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, TC>(acc, lds, job, N, p.ldc, wm, wn, [&] {
+    if (next_tile >= 0) {
+      set_rsrc(next);
+      set_offsets(next);
+#pragma unroll
+      for (int i = 0; i < LW; ++i) load1(0, i);
+    }
+  });
+  if (next_tile < 0) break;
+  __syncthreads();  // every wave is done with the staged output before stage 0 is rewritten
+  job = next;
+  zero_acc();
+  }
+}
+
 template <int BM, int BN, int BK, int STAGES, int WGM, int WGN, int PARTS>
 int launch_tile(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   const dim3 grid(args.total_tiles);
@@ -842,10 +1154,24 @@ int launch_w4(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
   return check_launch("gemm_bf16");
 }
 
+template <int BM, int BN>
+int launch_w4h(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
+  if (epilogue != IRIS_EPI_NONE)
+    return fail(IRIS_E_UNSUPPORTED, "gemm: the %dx%d tile has plain and bias epilogues only", BM, BN);
+  const int cus = device_cus();
+  if (c_dtype == IRIS_BF16)
+    gemm_w4h_kernel<BM, BN, IRIS_EPI_NONE, bf16, true><<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, 0,
+                                                         stream>>>(args);
+  else
+    gemm_w4h_kernel<BM, BN, IRIS_EPI_NONE, float, false><<<dim3(args.total_tiles), 256, 0, stream>>>(args);
+  return check_launch("gemm_bf16");
+}
+
 struct TileShape {
   int bm, bn, bk, stages, wgm, wgn, parts;
-  bool w4 = false;  // gemm_w4_kernel: four waves of 128 x 128, register-staged refills
-  bool swiglu() const { return (bn / wgn / 32) % 2 == 0; }
+  bool w4 = false;   // gemm_w4_kernel: four waves of 128 x 128, register-staged refills
+  bool w4h = false;  // gemm_w4h_kernel: four waves on the 16 x 16 x 32 MFMA, plain epilogue
+  bool swiglu() const { return !w4h && (bn / wgn / 32) % 2 == 0; }
 };
 // BM x BN output tile, BK-deep K tiles in a ring of `stages`, wgm x wgn waves, the refill of a
 // K tile spread over `parts` k-steps.
@@ -863,6 +1189,9 @@ constexpr TileShape kTiles[] = {
     {256, 256, 64, 2, 2, 2, 2},  // 10
     {256, 256, 64, 2, 2, 2, 1, true},  // 11: gemm_w4_kernel
     {192, 256, 64, 2, 2, 2, 1, true},  // 12: gemm_w4_kernel, 96 x 128 per wave
+    {288, 160, 64, 2, 2, 2, 1, false, true},  // 13: gemm_w4h_kernel, 144 x 80 per wave
+    {256, 160, 64, 2, 2, 2, 1, false, true},  // 14: gemm_w4h_kernel, 128 x 80 per wave
+    {128, 160, 64, 2, 2, 2, 1, false, true},  // 15: gemm_w4h_kernel, 64 x 80 per wave
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -872,6 +1201,9 @@ int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) 
   if constexpr (t.w4) {
     static_assert((t.bm == 256 || t.bm == 192) && t.bn == 256 && t.bk == 64, "gemm_w4_kernel tile");
     return launch_w4<t.bm>(args, c_dtype, epilogue, stream);
+  } else if constexpr (t.w4h) {
+    static_assert(t.bk == 64, "gemm_w4h_kernel tile");
+    return launch_w4h<t.bm, t.bn>(args, c_dtype, epilogue, stream);
   } else {
     return launch_tile<t.bm, t.bn, t.bk, t.stages, t.wgm, t.wgn, t.parts>(args, c_dtype, epilogue, stream);
   }
@@ -896,8 +1228,9 @@ struct Candidate {
   int tile, per_cu;
   double rate;
 };
-constexpr Candidate kCandidates[] = {{11, 1, 1.12}, {12, 1, 1.04}, {1, 1, 1.09},
-                                     {5, 1, 0.98}, {3, 1, 0.96}, {6, 2, 0.9}};
+constexpr Candidate kCandidates[] = {{11, 1, 1.12}, {12, 1, 1.04}, {1, 1, 1.09},   {5, 1, 0.98},
+                                     {3, 1, 0.96},  {6, 2, 0.9},   {13, 1, 1.04}, {14, 1, 1.04},
+                                     {15, 1, 0.9}};
 
 // Estimated time of one launch with candidate c (arbitrary units: tile area / rate per round).
 double launch_cost(const Candidate& c, const int* m, int groups, int n, int cus) {
@@ -908,18 +1241,27 @@ double launch_cost(const Candidate& c, const int* m, int groups, int n, int cus)
   return static_cast<double>((tiles + slots - 1) / slots) * t.bm * t.bn * c.per_cu / c.rate;
 }
 
-bool allowed(const Candidate& c, int epilogue) {
+// The MFMA shape of a launch depends on the output width and epilogue only, never on the row
+// count: the 16 x 16 x 32 MFMA sums 32 products per instruction, the 32 x 32 x 16 one 16, so
+// the two families round differently, and a row's result must not depend on the other rows of
+// the batch. Plain outputs of at most 2560 columns in whole 160-column tiles take the
+// 16 x 16 x 32 tiles, whose 160-wide columns divide 2560 and 1280 into 16 and 8.
+bool mfma16_family(int n, int epilogue) { return epilogue == IRIS_EPI_NONE && n % 160 == 0 && n <= 2560; }
+
+bool allowed(const Candidate& c, bool mfma16, int epilogue) {
   const TileShape t = kTiles[c.tile];
-  return !(epilogue == IRIS_EPI_SILU_MUL && !t.swiglu()) && !(epilogue == IRIS_EPI_SILU && t.w4);
+  return t.w4h == mfma16 && !(epilogue == IRIS_EPI_SILU_MUL && !t.swiglu()) &&
+         !(epilogue == IRIS_EPI_SILU && (t.w4 || t.w4h));
 }
 
-int pick_tile(const int* m, int groups, int n, int epilogue, int forced, double* cost_out = nullptr) {
+// (mfma16: the family of the whole output, also for the second part of a column split)
+int pick_tile(const int* m, int groups, int n, int epilogue, int forced, bool mfma16, double* cost_out = nullptr) {
   if (forced >= 0) return forced;
   const int cus = device_cus();
   int best = 11;
   double best_cost = 0.0;
   for (const Candidate& c : kCandidates) {
-    if (!allowed(c, epilogue)) continue;
+    if (!allowed(c, mfma16, epilogue)) continue;
     const double cost = launch_cost(c, m, groups, n, cus);
     if (best_cost == 0.0 || cost < best_cost) best = c.tile, best_cost = cost;
   }
@@ -941,9 +1283,10 @@ SplitPlan plan_split(const int* m, int groups, int n, int epilogue, int forced) 
   SplitPlan plan;
   const Candidate& c11 = kCandidates[0];
   // the first part always runs on tile 11: no split for an epilogue that tile does not have
-  if (forced >= 0 || !allowed(c11, epilogue)) return plan;
+  const bool mfma16 = mfma16_family(n, epilogue);
+  if (forced >= 0 || !allowed(c11, mfma16, epilogue)) return plan;
   double whole = 0.0;
-  plan.tile1 = pick_tile(m, groups, n, epilogue, -1, &whole);
+  plan.tile1 = pick_tile(m, groups, n, epilogue, -1, mfma16, &whole);
   const int cus = device_cus();
   const double extra_launch = 65536.0 / c11.rate * 0.05;
   double best = 0.98 * whole;  // a split must win by 2%
@@ -951,7 +1294,7 @@ SplitPlan plan_split(const int* m, int groups, int n, int epilogue, int forced) 
     const int n1 = 256 * c, n2 = n - n1;
     const double part1 = launch_cost(c11, m, groups, n1, cus);
     double part2 = 0.0;
-    const int t2 = pick_tile(m, groups, n2, epilogue, -1, &part2);
+    const int t2 = pick_tile(m, groups, n2, epilogue, -1, mfma16, &part2);
     const double cost = part1 + part2 + extra_launch;
     // on equal estimates the widest first part: more of the work on the 256 x 256 tile
     if (cost <= best) best = cost, plan.n1 = n1, plan.tile1 = 11, plan.tile2 = t2;
@@ -995,7 +1338,7 @@ int gemm_part(int groups, const void* const* a, const void* const* b, const floa
   args.total_tiles = begin;
   if (begin == 0) return IRIS_OK;
   IRIS_REQUIRE(epilogue != IRIS_EPI_SILU_MUL || shape.swiglu(), "gemm: tile %dx%d has no SwiGLU epilogue", bm, bn);
-  static_assert(kNumTiles == 13, "one case per tile shape");
+  static_assert(kNumTiles == 16, "one case per tile shape");
   switch (tile) {
 #define IRIS_TILE_CASE(I) \
   case I:                 \
@@ -1013,6 +1356,9 @@ int gemm_part(int groups, const void* const* a, const void* const* b, const floa
     IRIS_TILE_CASE(10)
     IRIS_TILE_CASE(11)
     IRIS_TILE_CASE(12)
+    IRIS_TILE_CASE(13)
+    IRIS_TILE_CASE(14)
+    IRIS_TILE_CASE(15)
 #undef IRIS_TILE_CASE
     default:
       return fail(IRIS_E_INVALID, "gemm: no tile shape %d", tile);
@@ -1050,7 +1396,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   const SplitPlan plan = plan_split(m, groups, n, epilogue, g_forced_tile);
   if (plan.n1 == 0)
     return gemm_part(groups, a, b, bias, c, m, c_dtype, n, k, lda, ldb, ldc, epilogue,
-                     pick_tile(m, groups, n, epilogue, g_forced_tile), stream);
+                     pick_tile(m, groups, n, epilogue, g_forced_tile, mfma16_family(n, epilogue)), stream);
   // two launches over columns [0, n1) and [n1, n): weight rows, bias entries and output columns
   // of the second start at n1 (n1 / 2 output columns for SwiGLU)
   const int rc = gemm_part(groups, a, b, bias, c, m, c_dtype, plan.n1, k, lda, ldb, ldc, epilogue, plan.tile1, stream);

@@ -350,7 +350,7 @@ def _gemm_ref(a, w, bias=None):
     return out if bias is None else out + bias.cpu()
 
 
-@pytest.mark.parametrize("tile", list(range(-1, 13)))
+@pytest.mark.parametrize("tile", list(range(-1, 16)))
 @pytest.mark.parametrize("mnk", [(300, 320, 128), (4096, 1280, 256), (1, 64, 64), (513, 260, 192)])
 def test_gemm_matches_fp32_reference(tile, mnk):
     m, n, k = mnk
@@ -394,6 +394,31 @@ def test_gemm_bf16_output_over_several_rounds(tile, shape, swiglu):
     else:
         want = prod
     close_bf16(out[rows], want)
+
+
+@pytest.mark.parametrize("tile", [13, 14, 15])
+@pytest.mark.parametrize("shape", [(4352, 2560, 6848), (4096, 1280, 4096), (4096, 16384, 2560)])
+def test_gemm_16x16_tiles_over_several_rounds(tile, shape):
+    """The four-wave tiles on the 16 x 16 x 32 MFMA (288 x 160, 256 x 160, 128 x 160) at step
+    shapes, persistent over one to thirteen rounds of 256 tiles for BF16 output (with and without
+    bias) and one tile per workgroup for FP32 output; against an FP32 product on sampled rows."""
+    m, n, k = shape
+    g = torch.Generator(device=DEV).manual_seed(19)
+    a = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (0.02 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g, device=DEV)
+    _lib.call("iris_gemm_force_tile", tile)
+    try:
+        out16 = K.linear(a, w)
+        out16b = K.linear(a, w, bias)
+        out32 = K.linear(a, w, bias, out_dtype=torch.float32)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    rows = torch.cat([torch.arange(0, m, 53), torch.tensor([m - 1])])
+    prod = a[rows].float().cpu() @ w.float().cpu().T
+    close_bf16(out16[rows], prod)
+    close_bf16(out16b[rows], prod + bias.cpu())
+    torch.testing.assert_close(out32[rows].cpu(), prod + bias.cpu(), rtol=1e-4, atol=2e-4)
 
 
 @pytest.mark.parametrize("rows,n,k,bias", [((4352,), 2560, 6848, False), ((4096, 256), 2560, 6848, False),
