@@ -1222,8 +1222,11 @@ int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) 
 // 256x192 0.96, 128x128 at two workgroups per CU 0.9. Measured slower in the step and
 // forced-only: the eight-wave 4-stage ring of 32-deep K tiles (8; 282 us on SwiGLU, although
 // 8% faster than tile 1 in back-to-back runs), and four waves with direct-to-LDS refills
-// (9, 10; 280-290 us).
-// The SwiGLU epilogue excludes the 192-column tiles, the SiLU epilogue the four-wave kernel.
+// (9, 10; 280-290 us). The 16 x 16 x 32 tiles compete among themselves only (mfma16_family
+// below): 288x160 (13) and 256x160 (14) 1.04 (one round of 256 tiles at 4352 and 4096 rows of
+// a 2560-column output; 4096 x 2560 x 6848 116 against 133 us on tile 12), 128x160 (15) 0.9
+// (one round at 4096 x 1280, 44-45 against 51-52 us for 128x128).
+// The SwiGLU epilogue excludes the 192-column tiles, the SiLU epilogue the four-wave kernels.
 struct Candidate {
   int tile, per_cu;
   double rate;
