@@ -784,11 +784,15 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
 }
 
 // Epilogue of the 16 x 16 x 32 MFMA layout: acc[i][j][e] = C[m, n] with n = tile + wave col +
-// 16 i + 4 (lane / 16) + e, m = tile + wave row + 16 j + lane % 16. BF16 output is staged
-// through the LDS ring in rows padded by 16 bytes (a row of 160 outputs is 80 dwords, so
-// without the pad rows r and r + 4 would share banks) and leaves in 16-byte row chunks; FP32
-// output is stored straight from the registers. `mid` as in store_tile.
-template <int BM, int BN, int WM, int WN, int FM, int FN, int NW, int RING, typename TC, typename Mid>
+// 16 i + 4 (lane / 16) + e, m = tile + wave row + 16 j + lane % 16. SwiGLU: in every 64-row
+// group of the packed weight the first 32 rows are w1 and the next 32 w3, so acc[i] (i % 4 < 2)
+// pairs with acc[i + 2] in the same lane, output column 32 (group) + 16 (i % 4) + 4 (lane / 16)
+// + e. BF16 output is staged through the LDS ring and leaves in 16-byte row chunks: rows of 160
+// outputs (80 dwords, so rows r and r + 4 would share banks) padded by 16 bytes, rows of 128 or
+// 256 (whose padded tile would not fit the ring) with 4-element unit u of row r at
+// u ^ 2 (r & 15), as store_tile. FP32 output is stored straight from the registers. `mid` as in
+// store_tile.
+template <int BM, int BN, int WM, int WN, int FM, int FN, int NW, int RING, int EPI, typename TC, typename Mid>
 __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, const TileJob& job, int N, long ldc,
                                              int wm, int wn, Mid&& mid) {
   const int tid = threadIdx.x;
@@ -798,45 +802,56 @@ __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, co
   const int M = job.m, tm = job.tm, tn = job.tn;
   const float* __restrict__ bias = job.bias;
   TC* __restrict__ C = static_cast<TC*>(job.c);
+  constexpr bool SWIGLU = EPI == IRIS_EPI_SILU_MUL;
+  static_assert(!SWIGLU || WN % 64 == 0, "SwiGLU pairs 32-column blocks inside one wave");
+  constexpr int OUT_N = SWIGLU ? BN / 2 : BN;  // output columns of the tile
+  const int n_out = SWIGLU ? N / 2 : N;
+  // tile-local output column of acc[i][.][0]
+  auto col = [&](int i) { return SWIGLU ? 32 * ((wn * WN) / 64 + i / 4) + 16 * (i % 4) + 4 * q4 : wn * WN + 16 * i + 4 * q4; };
+  // the four outputs of acc[i][j] (bias: the FP32 bias of those columns, zeros without one)
+  auto value = [&](int i, int j, int e, float bv) {
+    if constexpr (SWIGLU)
+      return silu(acc[i][j][e]) * acc[i + 2][j][e];
+    else
+      return acc[i][j][e] + bv;
+  };
   if constexpr (sizeof(TC) == 2) {
-    constexpr int PITCH = BN + 8;
+    constexpr bool SWZ = (OUT_N / 4) % 32 == 0;
+    constexpr int PITCH = SWZ ? OUT_N : OUT_N + 8;
     static_assert(BM * PITCH <= RING, "output tile must fit in the LDS ring");
     bf16* cl = lds;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
-      bf16* crow_l = cl + (wm * WM + 16 * j + l16) * PITCH;
+      const int r = wm * WM + 16 * j + l16;
+      bf16* crow_l = cl + r * PITCH;
 #pragma unroll
       for (int i = 0; i < FN; ++i) {
-        const int nl = wn * WN + 16 * i + 4 * q4;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
-        if (bias) {
-          const f32x4 bv = load4(bias + min(tn * BN + nl, N - 4));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += bv[e];
-        }
-        store_out4(crow_l + nl, v[0], v[1], v[2], v[3]);
+        if (SWIGLU && i % 4 >= 2) continue;
+        const int nl = col(i);
+        f32x4 bv = {};
+        if (!SWIGLU && bias) bv = load4(bias + min(tn * BN + nl, N - 4));
+        store_out4(crow_l + (SWZ ? 4 * ((nl / 4) ^ (2 * (r & 15))) : nl), value(i, j, 0, bv[0]), value(i, j, 1, bv[1]),
+                   value(i, j, 2, bv[2]), value(i, j, 3, bv[3]));
       }
     }
     __syncthreads();
     mid();
-    constexpr int CHUNKS = BN / 8;
-    const int col0 = tn * BN;
+    constexpr int CHUNKS = OUT_N / 8;
+    const int col0 = tn * OUT_N;
 #pragma unroll 4
     for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
       const int r = idx / CHUNKS;
       const int c = idx - r * CHUNKS;
       const int m = tm * BM + r;
       const int n0 = col0 + 8 * c;
-      if (m >= M || n0 >= N) continue;
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * PITCH + 8 * c);
+      if (m >= M || n0 >= n_out) continue;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * PITCH + 8 * (SWZ ? c ^ (r & 15) : c));
       TC* dst = C + static_cast<long>(m) * ldc + n0;
-      if (n0 + 8 <= N) {
+      if (n0 + 8 <= n_out) {
         *reinterpret_cast<bf16x8*>(dst) = v;
       } else {
-        *reinterpret_cast<bf16x4*>(dst) = bf16x4{v[0], v[1], v[2], v[3]};  // N % 4 == 0
+        *reinterpret_cast<bf16x4*>(dst) = bf16x4{v[0], v[1], v[2], v[3]};  // n_out % 4 == 0
       }
     }
     return;
@@ -845,20 +860,15 @@ __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, co
   for (int j = 0; j < FM; ++j) {
     const int m = tm * BM + wm * WM + 16 * j + l16;
     if (m >= M) continue;
-    TC* crow = C + static_cast<long>(m) * ldc;
+    TC* crow = C + static_cast<long>(m) * ldc + tn * OUT_N;
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
-      const int n0 = tn * BN + wn * WN + 16 * i + 4 * q4;
-      if (n0 >= N) continue;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e];
-      if (bias) {
-        const f32x4 bv = load4(bias + n0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += bv[e];
-      }
-      store_out4(crow + n0, v[0], v[1], v[2], v[3]);
+      if (SWIGLU && i % 4 >= 2) continue;
+      const int nl = col(i);
+      if (tn * OUT_N + nl >= n_out) continue;
+      f32x4 bv = {};
+      if (!SWIGLU && bias) bv = load4(bias + tn * BN + nl);
+      store_out4(crow + nl, value(i, j, 0, bv[0]), value(i, j, 1, bv[1]), value(i, j, 2, bv[2]), value(i, j, 3, bv[3]));
     }
   }
   mid();
@@ -913,7 +923,7 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
   static_assert(WM % 16 == 0 && WN % 16 == 0 && A_LOADS * RPL * NW == BM && B_LOADS * RPL * NW == BN,
                 "tile / wave split");
-  static_assert(EPI == IRIS_EPI_NONE, "plain or bias epilogue only");
+  static_assert(EPI == IRIS_EPI_NONE || EPI == IRIS_EPI_SILU_MUL, "plain, bias or SwiGLU epilogue");
   constexpr int W0 = (LW + 1) / 2;             // slots written to LDS (and reloaded) in k-step 0
   constexpr int W1 = LW - W0;                  // the rest, in k-step 1 before its barrier
   static_assert(NR + 2 * W0 <= NM && 2 * W1 + NR < NM && W1 > 0, "MFMAs per k-step");
@@ -1080,7 +1090,7 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   wait_vmcnt<0>();  // the repeated loads of the last K tile
   const int next_tile = PERSIST ? persistent_tile(p, round + 1) : -1;
   const TileJob next = next_tile >= 0 ? locate_tile_at<BM, BN>(p, next_tile) : job;
-  store_tile16<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, TC>(acc, lds, job, N, p.ldc, wm, wn, [&] {
+  store_tile16<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, [&] {
     if (next_tile >= 0) {
       set_rsrc(next);
       set_offsets(next);
@@ -1156,8 +1166,19 @@ int launch_w4(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
 
 template <int BM, int BN>
 int launch_w4h(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
+  const dim3 all(args.total_tiles);
+  if (epilogue == IRIS_EPI_SILU_MUL) {
+    // one tile per workgroup, as gemm_w4_kernel's SwiGLU form
+    if constexpr (BN / 2 % 64 == 0) {
+      if (c_dtype == IRIS_BF16)
+        gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, 0, stream>>>(args);
+      else
+        gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, float, false><<<all, 256, 0, stream>>>(args);
+      return check_launch("gemm_bf16");
+    }
+  }
   if (epilogue != IRIS_EPI_NONE)
-    return fail(IRIS_E_UNSUPPORTED, "gemm: the %dx%d tile has plain and bias epilogues only", BM, BN);
+    return fail(IRIS_E_UNSUPPORTED, "gemm: the %dx%d tile has no such epilogue", BM, BN);
   const int cus = device_cus();
   if (c_dtype == IRIS_BF16)
     gemm_w4h_kernel<BM, BN, IRIS_EPI_NONE, bf16, true><<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, 0,
@@ -1170,8 +1191,8 @@ int launch_w4h(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
 struct TileShape {
   int bm, bn, bk, stages, wgm, wgn, parts;
   bool w4 = false;   // gemm_w4_kernel: four waves of 128 x 128, register-staged refills
-  bool w4h = false;  // gemm_w4h_kernel: four waves on the 16 x 16 x 32 MFMA, plain epilogue
-  bool swiglu() const { return !w4h && (bn / wgn / 32) % 2 == 0; }
+  bool w4h = false;  // gemm_w4h_kernel: four waves on the 16 x 16 x 32 MFMA
+  bool swiglu() const { return w4h ? (bn / 2) % 64 == 0 : (bn / wgn / 32) % 2 == 0; }
 };
 // BM x BN output tile, BK-deep K tiles in a ring of `stages`, wgm x wgn waves, the refill of a
 // K tile spread over `parts` k-steps.
@@ -1192,6 +1213,8 @@ constexpr TileShape kTiles[] = {
     {288, 160, 64, 2, 2, 2, 1, false, true},  // 13: gemm_w4h_kernel, 144 x 80 per wave
     {256, 160, 64, 2, 2, 2, 1, false, true},  // 14: gemm_w4h_kernel, 128 x 80 per wave
     {128, 160, 64, 2, 2, 2, 1, false, true},  // 15: gemm_w4h_kernel, 64 x 80 per wave
+    {256, 256, 64, 2, 2, 2, 1, false, true},  // 16: gemm_w4h_kernel, 128 x 128 per wave
+    {192, 256, 64, 2, 2, 2, 1, false, true},  // 17: gemm_w4h_kernel, 96 x 128 per wave
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -1212,28 +1235,26 @@ int launch_index(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) 
 // Tile shape: the candidate with the least estimated time, rounds of workgroups over the
 // device's CUs (256 on MI355X; the last round costs as much as a full one) x tile area /
 // relative per-CU rate.
-// The rates are what the candidates do inside the denoise step (alternating runs of the whole
-// step on one box, the only measurement that ranked them reliably: back-to-back runs of one
-// GEMM ranked them differently): 256x256 with four 128x128 waves and register-staged refills
-// (11) 1.12, with eight 128x64 waves and direct-to-LDS refills (1) 1.09 (SwiGLU w1/w3 265
-// against 248 us per launch; the step 0.56-0.68 ms slower); 192x256 with four 96x128 waves
-// (12) 1.04 against 0.98 for eight 96x64 waves (5) (proj and w2: the step 0.47 ms faster; at
-// 1.08 the model would also move SwiGLU onto it, 4 us per launch slower than tile 11);
-// 256x192 0.96, 128x128 at two workgroups per CU 0.9. Measured slower in the step and
-// forced-only: the eight-wave 4-stage ring of 32-deep K tiles (8; 282 us on SwiGLU, although
-// 8% faster than tile 1 in back-to-back runs), and four waves with direct-to-LDS refills
-// (9, 10; 280-290 us). The 16 x 16 x 32 tiles compete among themselves only (mfma16_family
-// below): 288x160 (13) and 256x160 (14) 1.04 (one round of 256 tiles at 4352 and 4096 rows of
-// a 2560-column output; 4096 x 2560 x 6848 116 against 133 us on tile 12), 128x160 (15) 0.9
-// (one round at 4096 x 1280, 44-45 against 51-52 us for 128x128).
-// The SwiGLU epilogue excludes the 192-column tiles, the SiLU epilogue the four-wave kernels.
+// Plain, bias and SwiGLU outputs run on the four-wave tiles of the 16 x 16 x 32 MFMA. Their
+// rates are per-CU throughputs measured in one round of the microbenchmark (six weight copies,
+// one box), relative to the 32 x 32 x 16 four-wave 256 x 256 tile's 1.12: 256 x 256 (16) 1.17
+// (SwiGLU 4352 x 11520 x 2560, 765 tiles: 200 against 213 us on tile 11), 288 x 160 (13) 1.15,
+// 256 x 160 (14) 1.12, 192 x 256 (17) 1.05, 128 x 160 (15) 0.88.
+// The SiLU epilogue runs on the eight-wave tiles of the 32 x 32 x 16 MFMA, ranked inside the
+// denoise step (alternating runs of the whole step on one box): 256 x 256 with direct-to-LDS
+// refills (1) 1.09, 192 x 256 (5) 0.98, 256 x 192 (3) 0.96, 128 x 128 at two workgroups per CU
+// (6) 0.9. The four-wave 32 x 32 x 16 tiles (11, 12) are the q|k|v store's and forced-only;
+// so are the eight-wave 4-stage ring of 32-deep K tiles (8; 282 us on SwiGLU, although 8%
+// faster than tile 1 in back-to-back runs), and four waves with direct-to-LDS refills (9, 10;
+// 280-290 us).
 struct Candidate {
   int tile, per_cu;
   double rate;
 };
-constexpr Candidate kCandidates[] = {{11, 1, 1.12}, {12, 1, 1.04}, {1, 1, 1.09},   {5, 1, 0.98},
-                                     {3, 1, 0.96},  {6, 2, 0.9},   {13, 1, 1.04}, {14, 1, 1.04},
-                                     {15, 1, 0.9}};
+constexpr Candidate kCandidates[] = {{16, 1, 1.17}, {13, 1, 1.15}, {14, 1, 1.12}, {17, 1, 1.05}, {15, 1, 0.88},
+                                     {1, 1, 1.09},  {5, 1, 0.98},  {3, 1, 0.96},  {6, 2, 0.9}};
+constexpr int kSquare = 0;  // the 256 x 256 candidate of the 16 x 16 x 32 family
+static_assert(kCandidates[kSquare].tile == 16, "256 x 256 16 x 16 x 32 tile");
 
 // Estimated time of one launch with candidate c (arbitrary units: tile area / rate per round).
 double launch_cost(const Candidate& c, const int* m, int groups, int n, int cus) {
@@ -1244,63 +1265,60 @@ double launch_cost(const Candidate& c, const int* m, int groups, int n, int cus)
   return static_cast<double>((tiles + slots - 1) / slots) * t.bm * t.bn * c.per_cu / c.rate;
 }
 
-// The MFMA shape of a launch depends on the output width and epilogue only, never on the row
-// count: the 16 x 16 x 32 MFMA sums 32 products per instruction, the 32 x 32 x 16 one 16, so
-// the two families round differently, and a row's result must not depend on the other rows of
-// the batch. Plain outputs of at most 2560 columns in whole 160-column tiles take the
-// 16 x 16 x 32 tiles, whose 160-wide columns divide 2560 and 1280 into 16 and 8.
-bool mfma16_family(int n, int epilogue) { return epilogue == IRIS_EPI_NONE && n % 160 == 0 && n <= 2560; }
+// The MFMA shape of a launch depends on the epilogue only, never on the row count or the width:
+// the 16 x 16 x 32 MFMA sums 32 products per instruction, the 32 x 32 x 16 one 16, so the two
+// families round differently, and a row's result must not depend on the other rows of the
+// batch (nor a column's on where a column split falls).
+bool mfma16_family(int epilogue) { return epilogue == IRIS_EPI_NONE || epilogue == IRIS_EPI_SILU_MUL; }
 
-bool allowed(const Candidate& c, bool mfma16, int epilogue) {
+bool allowed(const Candidate& c, int epilogue) {
   const TileShape t = kTiles[c.tile];
-  return t.w4h == mfma16 && !(epilogue == IRIS_EPI_SILU_MUL && !t.swiglu()) &&
+  return t.w4h == mfma16_family(epilogue) && !(epilogue == IRIS_EPI_SILU_MUL && !t.swiglu()) &&
          !(epilogue == IRIS_EPI_SILU && (t.w4 || t.w4h));
 }
 
-// (mfma16: the family of the whole output, also for the second part of a column split)
-int pick_tile(const int* m, int groups, int n, int epilogue, int forced, bool mfma16, double* cost_out = nullptr) {
+int pick_tile(const int* m, int groups, int n, int epilogue, int forced, double* cost_out = nullptr) {
   if (forced >= 0) return forced;
   const int cus = device_cus();
-  int best = 11;
+  int best = -1;
   double best_cost = 0.0;
   for (const Candidate& c : kCandidates) {
-    if (!allowed(c, mfma16, epilogue)) continue;
+    if (!allowed(c, epilogue)) continue;
     const double cost = launch_cost(c, m, groups, n, cus);
-    if (best_cost == 0.0 || cost < best_cost) best = c.tile, best_cost = cost;
+    if (best < 0 || cost < best_cost) best = c.tile, best_cost = cost;
   }
   if (cost_out) *cost_out = best_cost;
   return best;
 }
 
 // Column split: when the last round of 256 x 256 tiles would leave many CUs idle, the first n1
-// columns run as whole rounds of 256 x 256 tiles (tile 11) and the rest as a second launch
+// columns run as whole rounds of 256 x 256 tiles (tile 16) and the rest as a second launch
 // with its own tile choice, e.g. SwiGLU 4352 x 13696: 765 tiles (3 rounds) + 207 tiles of
-// 192 x 256 (one round) instead of 918 tiles in 4 rounds; q|k|v|gate 4352 x 6400: 255 + 230
-// tiles instead of 425. A second launch is charged a fixed cost (~3 us). Measured in the
-// denoise step: 0.09 ms per step faster (the round model overstates the gain: the tiles of a
-// partly filled last round run faster than those of a full one). n1 = 0: no split.
+// 192 x 256 (one round) instead of 918 tiles in 4 rounds. A second launch is charged a fixed
+// cost (~3 us). Measured in the denoise step (on the 32 x 32 x 16 tiles then): 0.09 ms per step
+// faster (the round model overstates the gain: the tiles of a partly filled last round run
+// faster than those of a full one). n1 = 0: no split.
 struct SplitPlan {
-  int n1 = 0, tile1 = 11, tile2 = 11;
+  int n1 = 0, tile1 = 16, tile2 = 16;
 };
 SplitPlan plan_split(const int* m, int groups, int n, int epilogue, int forced) {
   SplitPlan plan;
-  const Candidate& c11 = kCandidates[0];
-  // the first part always runs on tile 11: no split for an epilogue that tile does not have
-  const bool mfma16 = mfma16_family(n, epilogue);
-  if (forced >= 0 || !allowed(c11, mfma16, epilogue)) return plan;
+  const Candidate& sq = kCandidates[kSquare];
+  // the first part always runs on the 256 x 256 tile: no split for an epilogue it does not have
+  if (forced >= 0 || !allowed(sq, epilogue)) return plan;
   double whole = 0.0;
-  plan.tile1 = pick_tile(m, groups, n, epilogue, -1, mfma16, &whole);
+  plan.tile1 = pick_tile(m, groups, n, epilogue, -1, &whole);
   const int cus = device_cus();
-  const double extra_launch = 65536.0 / c11.rate * 0.05;
+  const double extra_launch = 65536.0 / sq.rate * 0.05;
   double best = 0.98 * whole;  // a split must win by 2%
   for (int c = 1; c * 256 < n; ++c) {
     const int n1 = 256 * c, n2 = n - n1;
-    const double part1 = launch_cost(c11, m, groups, n1, cus);
+    const double part1 = launch_cost(sq, m, groups, n1, cus);
     double part2 = 0.0;
-    const int t2 = pick_tile(m, groups, n2, epilogue, -1, mfma16, &part2);
+    const int t2 = pick_tile(m, groups, n2, epilogue, -1, &part2);
     const double cost = part1 + part2 + extra_launch;
     // on equal estimates the widest first part: more of the work on the 256 x 256 tile
-    if (cost <= best) best = cost, plan.n1 = n1, plan.tile1 = 11, plan.tile2 = t2;
+    if (cost <= best) best = cost, plan.n1 = n1, plan.tile1 = sq.tile, plan.tile2 = t2;
   }
   return plan;
 }
@@ -1341,7 +1359,7 @@ int gemm_part(int groups, const void* const* a, const void* const* b, const floa
   args.total_tiles = begin;
   if (begin == 0) return IRIS_OK;
   IRIS_REQUIRE(epilogue != IRIS_EPI_SILU_MUL || shape.swiglu(), "gemm: tile %dx%d has no SwiGLU epilogue", bm, bn);
-  static_assert(kNumTiles == 16, "one case per tile shape");
+  static_assert(kNumTiles == 18, "one case per tile shape");
   switch (tile) {
 #define IRIS_TILE_CASE(I) \
   case I:                 \
@@ -1362,6 +1380,8 @@ int gemm_part(int groups, const void* const* a, const void* const* b, const floa
     IRIS_TILE_CASE(13)
     IRIS_TILE_CASE(14)
     IRIS_TILE_CASE(15)
+    IRIS_TILE_CASE(16)
+    IRIS_TILE_CASE(17)
 #undef IRIS_TILE_CASE
     default:
       return fail(IRIS_E_INVALID, "gemm: no tile shape %d", tile);
@@ -1399,7 +1419,7 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   const SplitPlan plan = plan_split(m, groups, n, epilogue, g_forced_tile);
   if (plan.n1 == 0)
     return gemm_part(groups, a, b, bias, c, m, c_dtype, n, k, lda, ldb, ldc, epilogue,
-                     pick_tile(m, groups, n, epilogue, g_forced_tile, mfma16_family(n, epilogue)), stream);
+                     pick_tile(m, groups, n, epilogue, g_forced_tile), stream);
   // two launches over columns [0, n1) and [n1, n): weight rows, bias entries and output columns
   // of the second start at n1 (n1 / 2 output columns for SwiGLU)
   const int rc = gemm_part(groups, a, b, bias, c, m, c_dtype, plan.n1, k, lda, ldb, ldc, epilogue, plan.tile1, stream);

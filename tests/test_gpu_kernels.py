@@ -350,7 +350,7 @@ def _gemm_ref(a, w, bias=None):
     return out if bias is None else out + bias.cpu()
 
 
-@pytest.mark.parametrize("tile", list(range(-1, 16)))
+@pytest.mark.parametrize("tile", list(range(-1, 18)))
 @pytest.mark.parametrize("mnk", [(300, 320, 128), (4096, 1280, 256), (1, 64, 64), (513, 260, 192)])
 def test_gemm_matches_fp32_reference(tile, mnk):
     m, n, k = mnk
@@ -369,7 +369,7 @@ def test_gemm_matches_fp32_reference(tile, mnk):
     close_bf16(out16, want - bias)
 
 
-@pytest.mark.parametrize("tile", [-1, 11, 12, 1])
+@pytest.mark.parametrize("tile", [-1, 11, 12, 1, 16, 17])
 @pytest.mark.parametrize("shape,swiglu", [((4352, 6400, 2560), False), ((4352, 13696, 2560), True),
                                           ((4096, 16384, 2560), False)])
 def test_gemm_bf16_output_over_several_rounds(tile, shape, swiglu):
@@ -478,7 +478,7 @@ def test_gemm_trunk_shapes(shape):
     torch.testing.assert_close(out[rows].cpu(), want, rtol=1e-4, atol=2e-4)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 4, 5, 6, 7, 8, 9, 10, 11, 12])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 4, 5, 6, 7, 8, 9, 10, 11, 12, 16, 17])
 def test_gemm_swiglu_epilogue_and_grouped_streams(tile):
     d, hidden = 256, 682
     hp = 704
