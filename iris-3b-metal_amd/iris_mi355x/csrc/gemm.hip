@@ -134,6 +134,128 @@ __device__ __forceinline__ int persistent_tile(const GemmArgs& p, int round) {
   return static_cast<int>(blockIdx.x) < count ? base + xcd_remap(blockIdx.x, count) : -1;
 }
 
+// kEpiQkRope, while the accumulators are staged: the Q and K gains of this tile's group go to
+// LDS (qk_gain, 256 floats) and thread r's rotary table row (tile row r) to registers.
+template <int BM>
+__device__ __forceinline__ void qk_tables(const TileJob& job, const QkRope& qk, float* qk_gain, f32x4 (&qk_cos)[16],
+                                          f32x4 (&qk_sin)[16]) {
+  const int tid = threadIdx.x;
+  const int M = job.m, tm = job.tm;
+  const float* __restrict__ gains = tid < 32 ? (job.group ? qk.q_weight1 : qk.q_weight0)
+                                             : (job.group ? qk.k_weight1 : qk.k_weight0);
+  if (tid < 64) store4(qk_gain + 4 * tid, load4(gains + 4 * (tid & 31)));
+  const int rpb = job.group ? qk.rows_per_batch1 : qk.rows_per_batch0;
+  const int mm = min(tm * BM + tid, M - 1);  // (rows past M read a valid row, unused)
+  const int b = mm / rpb;
+  const long pos = (job.group ? qk.dst_offset1 : qk.dst_offset0) + (mm - b * rpb);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    qk_cos[i] = load4(qk.cos + pos * 64 + 4 * i);
+    qk_sin[i] = load4(qk.sin + pos * 64 + 4 * i);
+  }
+}
+
+// kEpiQkRope, once the BF16 tile is staged in LDS (256 outputs per row, 4-element unit u of row
+// r at u ^ 2 (r & 15)): thread r normalises and rotates the Q / K heads of tile row r in place
+// (two 128-column heads per row, 16 chunks each), then the tile leaves in 16-byte row chunks:
+// Q / K rows to q / k at their token's position, the V columns to C (or transposed to vt).
+template <int BM, int NW>
+__device__ __forceinline__ void qk_store(bf16* cl, const TileJob& job, int N, long ldc, const QkRope& qk,
+                                         const float* qk_gain, const f32x4 (&qk_cos)[16], const f32x4 (&qk_sin)[16]) {
+  constexpr int OUT_N = 256, MASK = 15, CHUNKS = 32;
+  const int tid = threadIdx.x;
+  const int M = job.m, tm = job.tm, tn = job.tn;
+  bf16* __restrict__ C = static_cast<bf16*>(job.c);
+  const int n_out = N;
+  const int col0 = tn * OUT_N;
+  const int nq = qk.heads * 128, nqk = nq + qk.kv_heads * 128;
+  const int rpb = job.group ? qk.rows_per_batch1 : qk.rows_per_batch0;
+  const int dst_offset = job.group ? qk.dst_offset1 : qk.dst_offset0;
+  if (tm * BM + tid < M) {
+    bf16* row = cl + tid * OUT_N;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int n0 = col0 + 128 * hh;  // (the same for the whole workgroup)
+      if (n0 >= n_out || n0 >= nqk) continue;
+      const float* gain = qk_gain + (n0 < nq ? 0 : 128);
+      auto chunk = [&](int c) { return reinterpret_cast<bf16x8*>(row + 8 * ((16 * hh + c) ^ (tid & MASK))); };
+      float ss[16];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const bf16x8 v = *chunk(c);
+        float a[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = to_f32(v[e]);
+        ss[c] = head_chunk_sq(a);
+      }
+      const float rs = head_rms_scale(head_sum_tree(ss), qk.eps);
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {  // (read again: keeping the head in registers spills)
+        const bf16x8 v = *chunk(c);
+        float a[8], w[8], y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = to_f32(v[e]);
+        load8(gain + 8 * c, w);
+        head_scale_rope(a, rs, w, qk_cos[c], qk_sin[c], y);
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = from_f32<bf16>(y[e]);
+        *chunk(c) = o;
+      }
+    }
+  }
+  __syncthreads();
+  if (qk.vt) {
+    // V heads transposed: thread t gathers dim t % 128 for positions 8 c .. 8 c + 7 of the
+    // tile's tokens (each 16-position group in the slot order of vt_slot), c = t / 128 + 2 j;
+    // a wave's lanes read 64 consecutive dims of one tile row (no LDS bank conflicts) and
+    // store 16 bytes each into 64 rows of vt
+    const int b = (tm * BM) / rpb;
+    const long p0 = dst_offset + (tm * BM - b * rpb);  // a multiple of 16
+    const int d = tid & 127;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int n0 = col0 + 128 * hh;  // (the same for the whole workgroup)
+      if (n0 < nqk || n0 >= n_out) continue;
+      const int vh = (n0 - nqk) >> 7;
+      const int col = 128 * hh + d;
+      bf16* vtd = qk.vt + ((static_cast<long>(b) * qk.kv_heads + vh) * 128 + d) * static_cast<long>(qk.n_vt) + p0;
+#pragma unroll 4
+      for (int j = 0; j < 16; ++j) {
+        const int c8 = (tid >> 7) + 2 * j;  // (wave-uniform)
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = vt_slot(8 * c8 + e);  // tile row holding this position's token
+          o[e] = cl[i * OUT_N + 4 * ((col >> 2) ^ (2 * (i & MASK))) + (col & 3)];
+        }
+        *reinterpret_cast<bf16x8*>(vtd + 8 * c8) = o;
+      }
+    }
+  }
+#pragma unroll 4
+  for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
+    const int r = idx / CHUNKS;
+    const int c = idx - r * CHUNKS;
+    const int m = tm * BM + r;
+    const int n0 = col0 + 8 * c;
+    if (m >= M || n0 >= n_out) continue;
+    if (n0 >= nqk && qk.vt) continue;  // (written transposed above)
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * OUT_N + 8 * (c ^ (r & MASK)));
+    if (n0 >= nqk) {  // V heads
+      *reinterpret_cast<bf16x8*>(C + static_cast<long>(m) * ldc + n0) = v;
+      continue;
+    }
+    const bool is_q = n0 < nq;
+    const int head = (is_q ? n0 : n0 - nq) >> 7;
+    const int b = m / rpb;
+    const long pos = dst_offset + (m - b * rpb);
+    bf16* dst = is_q ? qk.q + ((static_cast<long>(b) * qk.heads + head) * qk.n_dst + pos) * 128
+                     : qk.k + ((static_cast<long>(b) * qk.kv_heads + head) * qk.n_dst + pos) * 128;
+    *reinterpret_cast<bf16x8*>(dst + 8 * (c & 15)) = v;
+  }
+}
+
 // Epilogue shared by the kernels: acc[i][j][r] = C[m, n] with n = tile + wave col + 32 i +
 // 8 (r / 4) + 4 g + r % 4, m = tile + wave row + 32 j + l32; BF16 output through the LDS ring.
 // `mid` runs once the accumulators are no longer needed (after they are staged in LDS, or at
@@ -167,18 +289,7 @@ __device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, con
     [[maybe_unused]] f32x4 qk_cos[EPI == kEpiQkRope ? 16 : 1], qk_sin[EPI == kEpiQkRope ? 16 : 1];
     if constexpr (EPI == kEpiQkRope) {
       static_assert(BM == 64 * NW, "one tile row per thread");
-      const float* __restrict__ gains = tid < 32 ? (job.group ? qk.q_weight1 : qk.q_weight0)
-                                                 : (job.group ? qk.k_weight1 : qk.k_weight0);
-      if (tid < 64) store4(qk_gain + 4 * tid, load4(gains + 4 * (tid & 31)));
-      const int rpb = job.group ? qk.rows_per_batch1 : qk.rows_per_batch0;
-      const int mm = min(tm * BM + tid, M - 1);  // (rows past M read a valid row, unused)
-      const int b = mm / rpb;
-      const long pos = (job.group ? qk.dst_offset1 : qk.dst_offset0) + (mm - b * rpb);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        qk_cos[i] = load4(qk.cos + pos * 64 + 4 * i);
-        qk_sin[i] = load4(qk.sin + pos * 64 + 4 * i);
-      }
+      qk_tables<BM>(job, qk, qk_gain, qk_cos, qk_sin);
     }
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
@@ -225,96 +336,8 @@ __device__ __forceinline__ void store_tile(f32x16 (&acc)[FN][FM], bf16* lds, con
     const int n_out = EPI == IRIS_EPI_SILU_MUL ? N / 2 : N;
     const int col0 = tn * OUT_N;
     if constexpr (EPI == kEpiQkRope) {
-      // Thread r normalises and rotates the Q / K heads of tile row r in place (two 128-column
-      // heads per row, 16 chunks each), then the tile leaves in 16-byte row chunks: Q / K rows to
-      // q / k at their token's position, the V columns to C.
       static_assert(OUT_N == 256 && MASK == 15 && CHUNKS == 32, "two heads of 16 chunks per row");
-      const int nq = qk.heads * 128, nqk = nq + qk.kv_heads * 128;
-      const int rpb = job.group ? qk.rows_per_batch1 : qk.rows_per_batch0;
-      const int dst_offset = job.group ? qk.dst_offset1 : qk.dst_offset0;
-      if (tm * BM + tid < M) {
-        bf16* row = cl + tid * OUT_N;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int n0 = col0 + 128 * hh;  // (the same for the whole workgroup)
-          if (n0 >= n_out || n0 >= nqk) continue;
-          const float* gain = qk_gain + (n0 < nq ? 0 : 128);
-          auto chunk = [&](int c) { return reinterpret_cast<bf16x8*>(row + 8 * ((16 * hh + c) ^ (tid & MASK))); };
-          float ss[16];
-#pragma unroll
-          for (int c = 0; c < 16; ++c) {
-            const bf16x8 v = *chunk(c);
-            float a[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a[e] = to_f32(v[e]);
-            ss[c] = head_chunk_sq(a);
-          }
-          const float rs = head_rms_scale(head_sum_tree(ss), qk.eps);
-#pragma unroll
-          for (int c = 0; c < 16; ++c) {  // (read again: keeping the head in registers spills)
-            const bf16x8 v = *chunk(c);
-            float a[8], w[8], y[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) a[e] = to_f32(v[e]);
-            load8(gain + 8 * c, w);
-            head_scale_rope(a, rs, w, qk_cos[c], qk_sin[c], y);
-            bf16x8 o;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = from_f32<bf16>(y[e]);
-            *chunk(c) = o;
-          }
-        }
-      }
-      __syncthreads();
-      if (qk.vt) {
-        // V heads transposed: thread t gathers dim t % 128 for positions 8 c .. 8 c + 7 of the
-        // tile's tokens (each 16-position group in the slot order of vt_slot), c = t / 128 + 2 j;
-        // a wave's lanes read 64 consecutive dims of one tile row (no LDS bank conflicts) and
-        // store 16 bytes each into 64 rows of vt
-        const int b = (tm * BM) / rpb;
-        const long p0 = dst_offset + (tm * BM - b * rpb);  // a multiple of 16
-        const int d = tid & 127;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int n0 = col0 + 128 * hh;  // (the same for the whole workgroup)
-          if (n0 < nqk || n0 >= n_out) continue;
-          const int vh = (n0 - nqk) >> 7;
-          const int col = 128 * hh + d;
-          bf16* vtd = qk.vt + ((static_cast<long>(b) * qk.kv_heads + vh) * 128 + d) * static_cast<long>(qk.n_vt) + p0;
-#pragma unroll 4
-          for (int j = 0; j < 16; ++j) {
-            const int c8 = (tid >> 7) + 2 * j;  // (wave-uniform)
-            bf16x8 o;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int i = vt_slot(8 * c8 + e);  // tile row holding this position's token
-              o[e] = cl[i * OUT_N + 4 * ((col >> 2) ^ (2 * (i & MASK))) + (col & 3)];
-            }
-            *reinterpret_cast<bf16x8*>(vtd + 8 * c8) = o;
-          }
-        }
-      }
-#pragma unroll 4
-      for (int idx = tid; idx < BM * CHUNKS; idx += 64 * NW) {
-        const int r = idx / CHUNKS;
-        const int c = idx - r * CHUNKS;
-        const int m = tm * BM + r;
-        const int n0 = col0 + 8 * c;
-        if (m >= M || n0 >= n_out) continue;
-        if (n0 >= nqk && qk.vt) continue;  // (written transposed above)
-        const bf16x8 v = *reinterpret_cast<const bf16x8*>(cl + r * OUT_N + 8 * (c ^ (r & MASK)));
-        if (n0 >= nqk) {  // V heads
-          *reinterpret_cast<bf16x8*>(C + static_cast<long>(m) * ldc + n0) = v;
-          continue;
-        }
-        const bool is_q = n0 < nq;
-        const int head = (is_q ? n0 : n0 - nq) >> 7;
-        const int b = m / rpb;
-        const long pos = dst_offset + (m - b * rpb);
-        bf16* dst = is_q ? qk.q + ((static_cast<long>(b) * qk.heads + head) * qk.n_dst + pos) * 128
-                         : qk.k + ((static_cast<long>(b) * qk.kv_heads + head) * qk.n_dst + pos) * 128;
-        *reinterpret_cast<bf16x8*>(dst + 8 * (c & 15)) = v;
-      }
+      qk_store<BM, NW>(cl, job, N, ldc, qk, qk_gain, qk_cos, qk_sin);
       return;
     }
 #pragma unroll 4
@@ -794,7 +817,7 @@ __global__ __launch_bounds__(256) void gemm_w4_kernel(GemmArgs p) {
 // store_tile.
 template <int BM, int BN, int WM, int WN, int FM, int FN, int NW, int RING, int EPI, typename TC, typename Mid>
 __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, const TileJob& job, int N, long ldc,
-                                             int wm, int wn, Mid&& mid) {
+                                             int wm, int wn, const QkRope& qk, Mid&& mid) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int l16 = lane & 15;
@@ -821,6 +844,12 @@ __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, co
     static_assert(BM * PITCH <= RING, "output tile must fit in the LDS ring");
     bf16* cl = lds;
     __syncthreads();
+    __shared__ float qk_gain[EPI == kEpiQkRope ? 256 : 1];
+    [[maybe_unused]] f32x4 qk_cos[EPI == kEpiQkRope ? 16 : 1], qk_sin[EPI == kEpiQkRope ? 16 : 1];
+    if constexpr (EPI == kEpiQkRope) {
+      static_assert(BM == 64 * NW && BN == 256 && SWZ, "one 256-wide tile row per thread");
+      qk_tables<BM>(job, qk, qk_gain, qk_cos, qk_sin);
+    }
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int r = wm * WM + 16 * j + l16;
@@ -837,6 +866,10 @@ __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, co
     }
     __syncthreads();
     mid();
+    if constexpr (EPI == kEpiQkRope) {
+      qk_store<BM, NW>(cl, job, N, ldc, qk, qk_gain, qk_cos, qk_sin);
+      return;
+    }
     constexpr int CHUNKS = OUT_N / 8;
     const int col0 = tn * OUT_N;
 #pragma unroll 4
@@ -923,7 +956,7 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
   static_assert(WM % 16 == 0 && WN % 16 == 0 && A_LOADS * RPL * NW == BM && B_LOADS * RPL * NW == BN,
                 "tile / wave split");
-  static_assert(EPI == IRIS_EPI_NONE || EPI == IRIS_EPI_SILU_MUL, "plain, bias or SwiGLU epilogue");
+  static_assert(EPI == IRIS_EPI_NONE || EPI == IRIS_EPI_SILU_MUL || EPI == kEpiQkRope, "plain, bias, SwiGLU or q|k|v epilogue");
   constexpr int W0 = (LW + 1) / 2;             // slots written to LDS (and reloaded) in k-step 0
   constexpr int W1 = LW - W0;                  // the rest, in k-step 1 before its barrier
   static_assert(NR + 2 * W0 <= NM && 2 * W1 + NR < NM && W1 > 0, "MFMAs per k-step");
@@ -1090,7 +1123,7 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   wait_vmcnt<0>();  // the repeated loads of the last K tile
   const int next_tile = PERSIST ? persistent_tile(p, round + 1) : -1;
   const TileJob next = next_tile >= 0 ? locate_tile_at<BM, BN>(p, next_tile) : job;
-  store_tile16<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, [&] {
+  store_tile16<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, p.qk, [&] {
     if (next_tile >= 0) {
       set_rsrc(next);
       set_offsets(next);
@@ -1166,6 +1199,7 @@ int launch_w4(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
 
 template <int BM, int BN>
 int launch_w4h(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
+  if (epilogue == IRIS_EPI_SILU) return fail(IRIS_E_UNSUPPORTED, "gemm: the four-wave tiles have no SiLU epilogue");
   const dim3 all(args.total_tiles);
   if (epilogue == IRIS_EPI_SILU_MUL) {
     // one tile per workgroup, as gemm_w4_kernel's SwiGLU form
@@ -1174,6 +1208,13 @@ int launch_w4h(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
         gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, 0, stream>>>(args);
       else
         gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, float, false><<<all, 256, 0, stream>>>(args);
+      return check_launch("gemm_bf16");
+    }
+  }
+  if (epilogue == kEpiQkRope) {
+    // one tile per workgroup: the next tile's loads in flight would spill the store's registers
+    if constexpr (BM == 256 && BN == 256) {
+      gemm_w4h_kernel<BM, BN, kEpiQkRope, bf16, false><<<all, 256, 0, stream>>>(args);
       return check_launch("gemm_bf16");
     }
   }
@@ -1254,6 +1295,10 @@ struct Candidate {
 constexpr Candidate kCandidates[] = {{16, 1, 1.17}, {13, 1, 1.15}, {14, 1, 1.12}, {17, 1, 1.05}, {15, 1, 0.88},
                                      {1, 1, 1.09},  {5, 1, 0.98},  {3, 1, 0.96},  {6, 2, 0.9}};
 constexpr int kSquare = 0;  // the 256 x 256 candidate of the 16 x 16 x 32 family
+// The q|k|v projection's store (one tile row per thread, two heads per row) runs on the
+// 256 x 256 tile of the family of the plain GEMM, so its outputs are bitwise those of
+// iris_gemm_bf16 followed by iris_qkv_prepare.
+constexpr int kQkRopeTile = 16;
 static_assert(kCandidates[kSquare].tile == 16, "256 x 256 16 x 16 x 32 tile");
 
 // Estimated time of one launch with candidate c (arbitrary units: tile area / rate per round).
@@ -1506,7 +1551,7 @@ extern "C" int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const vo
   qk.eps = eps;
   qk.vt = static_cast<bf16*>(vt);
   qk.n_vt = static_cast<int>(n_vt);
-  return gemm_part(groups, a, b, nullptr, c, m, IRIS_BF16, n, k, lda, ldb, ldc, kEpiQkRope, 11, stream, &qk);
+  return gemm_part(groups, a, b, nullptr, c, m, IRIS_BF16, n, k, lda, ldb, ldc, kEpiQkRope, kQkRopeTile, stream, &qk);
 }
 
 extern "C" int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n,
