@@ -976,18 +976,25 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
 
   // load i: A rows (w A_LOADS + i) RPL .. + RPL for i < A_LOADS, B rows (w B_LOADS + i -
   // A_LOADS) RPL .. for the rest; lane l fetches the chunk that belongs at byte 16 l of that
-  // 1 KB block in LDS. Byte offsets.
+  // 1 KB block in LDS. Byte offset of load j of an operand: a per-lane part shared by the loads
+  // of the same parity (a row's swizzle depends on (row / 2) % 8, and j + 2 is 16 rows further),
+  // plus (j & ~1) RPL rows and the K position in an SGPR: four address VGPRs instead of one per
+  // load. Rows past an operand's end are not clamped: the buffer's range check returns zeros
+  // (or, past 2^32 bytes, wraps inside the buffer), which reach only output rows and columns
+  // that are not stored.
   const int ld_r = lane / CPR;
   const int ld_p = lane % CPR;
-  int off[LW];
+  const unsigned lda2 = 2u * static_cast<unsigned>(p.lda), ldb2 = 2u * static_cast<unsigned>(p.ldb);
+  unsigned voff[2][2];  // [operand][parity]
   auto set_offsets = [&](const TileJob& jb) {
 #pragma unroll
-    for (int i = 0; i < LW; ++i) {
-      const bool is_a = i < A_LOADS;
-      const int r = (is_a ? w * A_LOADS + i : w * B_LOADS + i - A_LOADS) * RPL + ld_r;
-      off[i] = 2 * (is_a ? min(jb.tm * BM + r, jb.m - 1) * static_cast<int>(p.lda) + 8 * (ld_p ^ swz<BK>(r))
-                         : min(jb.tn * BN + r, N - 1) * static_cast<int>(p.ldb) + 8 * (ld_p ^ swz<BK>(r)));
-    }
+    for (int op = 0; op < 2; ++op)
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        const int r = (w * (op ? B_LOADS : A_LOADS) + par) * RPL + ld_r;  // row inside the tile
+        const unsigned row = static_cast<unsigned>((op ? jb.tn * BN : jb.tm * BM) + r);
+        voff[op][par] = row * (op ? ldb2 : lda2) + 16u * static_cast<unsigned>(ld_p ^ swz<BK>(r));
+      }
   };
   set_offsets(job);
   bf16x8 staged[LW];
@@ -998,8 +1005,11 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   };
   set_rsrc(job);
   auto load1 = [&](int kt, int i) {
-    staged[i] =
-        __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(i < A_LOADS ? rsrc_a : rsrc_b, off[i], kt * BK * 2, 0));
+    const int op = i < A_LOADS ? 0 : 1;
+    const int j = op ? i - A_LOADS : i;
+    const unsigned soff = static_cast<unsigned>(kt * BK * 2) + static_cast<unsigned>((j & ~1) * RPL) * (op ? ldb2 : lda2);
+    staged[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(op ? rsrc_b : rsrc_a, voff[op][j & 1],
+                                                                                static_cast<int>(soff), 0));
   };
   auto write1 = [&](int stage, int i) {
     bf16* blk = lds + stage * STAGE +
