@@ -8,7 +8,7 @@ N(0, 1) prepared text tokens (the text adapter is outside the step, as in the re
 (recorded during the warm-up steps), the Euler update launched after it.
 
 Prints one JSON line. Besides the driver's fields it carries:
-- ``roofline``: the dominant kernel, the trunk's SwiGLU w1/w3 GEMM (``gemm_w4_kernel`` with the
+- ``roofline``: the dominant kernel, the trunk's SwiGLU w1/w3 GEMM (``gemm_w4h_kernel`` with the
   SwiGLU epilogue, M x 2*6826 x 2560 per block), from a second timed pass of the same steps
   launched eagerly so that every GEMM launch can be bracketed by HIP events on its stream
   (``eager_ms_per_step``): ``achieved`` = algorithmic 2*M*N*K (unpadded) over the launches'
@@ -424,10 +424,10 @@ def main() -> None:
                 "launches": launches, "avg_launch_us": 1000.0 * ms / max(launches, 1),
                 "flop_per_launch": fl / max(launches, 1)}
 
-    roofline = {"bound": "mfma", "kernel": "gemm_w4_kernel<256, SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
+    roofline = {"bound": "mfma", "kernel": "gemm_w4h_kernel<256, 256, SwiGLU> + <192, 256, SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
                 **rate(True), "traffic": profiled_traffic(),
                 "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
-    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4_kernel incl. the q|k|v store with Q/K norm + RoPE, gemm_kernel)", **rate(False)}
+    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4h_kernel incl. the q|k|v store with Q/K norm + RoPE)", **rate(False)}
     att_source = ATTENTION_TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if ATTENTION_TRAFFIC_PROFILE.exists() else None
     attention = {"kernel": "flash_attn_kernel, trunk joint attention (20 query / 5 K/V heads)",
                  **timer.attention_summary(cfg.num_heads),
