@@ -861,6 +861,21 @@ def test_gemv_with_core_biases(j):
     torch.testing.assert_close(out2.cpu(), F.silu(x @ w.float().T + bias), rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("n,k,b", [(15360, 2560, 1), (100, 4096, 5), (13, 8, 3), (7, 520, 4)])
+def test_gemv_shapes(n, k, b):
+    """The adaLN-core shape (15360 x 2560), the largest K (4096: eight 16-byte chunks per lane),
+    batches past four (two launches), row counts that leave a workgroup's last rows empty and a
+    K that leaves some lanes without a chunk."""
+    g = gen(12)
+    w = (0.05 * torch.randn(n, k, generator=g)).to(torch.bfloat16)
+    x = torch.randn(b, k, generator=g)
+    bias = torch.randn(n, generator=g)
+    out = torch.empty(b, n, device=DEV)
+    K.gemv(w.to(DEV), x.to(DEV), bias.to(DEV), out)
+    want = x.double() @ w.double().T + bias.double()
+    torch.testing.assert_close(out.cpu().double(), want, rtol=1e-5, atol=1e-4)
+
+
 def test_timestep_features():
     from iris_mi355x import tables
 
