@@ -747,6 +747,26 @@ def test_gemm_silu_epilogue_at_batched_adapter_shapes(m):
     close_bf16(out16, want)
 
 
+@pytest.mark.parametrize("tile", [-1, 16, 17, 11])
+def test_gemm_swiglu_fp32_output(tile):
+    """SwiGLU into an FP32 output (stored straight from the accumulators, no LDS staging), one
+    tile per workgroup; rows and hidden units not multiples of the tile."""
+    d, hidden, hp = 192, 300, 320
+    g = gen(13)
+    w1, w3 = 0.05 * torch.randn(hidden, d, generator=g), 0.05 * torch.randn(hidden, d, generator=g)
+    packed = K.pack_swiglu(w1, w3, hp).to(torch.bfloat16)
+    x = torch.randn(333, d, generator=g).to(torch.bfloat16)
+    _lib.call("iris_gemm_force_tile", tile)
+    try:
+        out = K.linear(x.to(DEV), packed.to(DEV), swiglu=True, out_dtype=torch.float32)
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    a = x.float() @ w1.to(torch.bfloat16).float().T
+    b = x.float() @ w3.to(torch.bfloat16).float().T
+    torch.testing.assert_close(out[:, :hidden].cpu(), F.silu(a) * b, rtol=1e-4, atol=1e-4)
+    assert torch.all(out[:, hidden:].cpu() == 0)
+
+
 @pytest.mark.parametrize("tile", [11, 16, 13])
 def test_gemm_silu_is_refused_by_the_four_wave_tile(tile):
     a = torch.zeros(64, 64, device=DEV, dtype=torch.bfloat16)
