@@ -1,20 +1,25 @@
 // BF16 GEMM on gfx950 MFMA: C[m, n] = sum_k A[m, k] * B[n, k] (+ bias[n]), FP32 accumulate.
 //
 // Both operands are K-contiguous ("NT"), the natural layout of nn.Linear weights, so every
-// MFMA operand fragment is one 16-byte LDS read. A workgroup computes a BM x BN tile with
-// WGM x WGN waves; each wave owns a (BM/WGM) x (BN/WGN) block of v_mfma_f32_32x32x16_bf16
-// results. The weight fragment is the MFMA's A operand and the activation fragment its B
-// operand, so each lane ends up holding four consecutive output columns of one row: the
-// epilogue stores 8 (BF16) or 16 (FP32) contiguous bytes per lane.
+// MFMA operand fragment is one 16-byte LDS read. The weight fragment is the MFMA's A operand
+// and the activation fragment its B operand, so each lane ends up holding four consecutive
+// output columns of one row. LDS tiles are XOR-swizzled so the fragment reads are bank-conflict
+// free, and workgroup ids are remapped so that the tiles running concurrently on one XCD form
+// an 8 x 4 block and share their operands through that XCD's L2.
 //
-// Data path: K tiles go global -> LDS with buffer_load_dwordx4 ... lds (no register staging;
-// a 32-bit VGPR byte offset per load, the K position in an SGPR, the LDS target wave-uniform, so
-// a refill costs no 64-bit address arithmetic and no VGPR-to-M0 moves) into a ring of STAGES
-// buffers, XOR-swizzled so the MFMA fragment reads are bank-conflict
-// free. The fragments of the next k-step are read while the current MFMAs run, and the
-// wait + barrier for the next K tile is placed before the last k-step of the current one.
-// Workgroup ids are remapped so that the tiles running concurrently on one XCD form an
-// 8 x 4 block and share their operands through that XCD's L2.
+// Three kernels:
+// - gemm_w4h_kernel (the default for plain, bias and SwiGLU outputs and the q|k|v store): four
+//   waves, one per SIMD, in a 2 x 2 grid of v_mfma_f32_16x16x32_bf16 blocks; K tiles staged
+//   through registers (16-byte buffer loads two K tiles ahead) into a 2-stage LDS ring;
+//   288 x 160, 256 x 160, 128 x 160, 256 x 256 and 192 x 256 tiles.
+// - gemm_w4_kernel: the same design on v_mfma_f32_32x32x16_bf16 (256 x 256, 192 x 256),
+//   forced-only (a tuning and test reference).
+// - gemm_kernel: eight waves, K tiles global -> LDS with buffer_load_dwordx4 ... lds into a ring
+//   of STAGES buffers (no register staging; a 32-bit VGPR byte offset per load, the K position
+//   in an SGPR, the LDS target wave-uniform), v_mfma_f32_32x32x16_bf16; the SiLU epilogue's
+//   kernel (the four-wave kernels have none).
+// The MFMA shape of a launch follows from its epilogue alone (mfma16_family), so a row's
+// result never depends on the row count or the tile chosen.
 #include "iris_common.hpp"
 
 #include <type_traits>
