@@ -835,7 +835,9 @@ __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, co
   constexpr int OUT_N = SWIGLU ? BN / 2 : BN;  // output columns of the tile
   const int n_out = SWIGLU ? N / 2 : N;
   // tile-local output column of acc[i][.][0]
-  auto col = [&](int i) { return SWIGLU ? 32 * ((wn * WN) / 64 + i / 4) + 16 * (i % 4) + 4 * q4 : wn * WN + 16 * i + 4 * q4; };
+  auto col = [&](int i) {
+    return SWIGLU ? 32 * ((wn * WN) / 64 + i / 4) + 16 * (i % 4) + 4 * q4 : wn * WN + 16 * i + 4 * q4;
+  };
   // the four outputs of acc[i][j] (bias: the FP32 bias of those columns, zeros without one)
   auto value = [&](int i, int j, int e, float bv) {
     if constexpr (SWIGLU)
@@ -913,7 +915,7 @@ __device__ __forceinline__ void store_tile16(f32x4 (&acc)[FN][FM], bf16* lds, co
 }
 
 // v_mfma_f32_16x16x32_bf16 accumulating in place, c += a b. Written as inline assembly: with the
-// builtin, the register allocator rotates the 40-odd four-register accumulator tuples of
+// builtin, the register allocator rotates the 40 to 64 four-register accumulator tuples of
 // gemm_w4h_kernel between registers inside the K loop (hundreds of accumulator moves per K
 // tile). An asm statement is also an ordering point for memory operations, so the LDS reads and
 // writes and the global loads between these MFMAs issue where the source places them. The
@@ -939,10 +941,11 @@ __device__ __forceinline__ void mfma16_acc(f32x4& c, const bf16x8& a, const bf16
 
 // Four waves (one per SIMD) in a 2 x 2 grid over a BM x BN tile on v_mfma_f32_16x16x32_bf16,
 // refilled as gemm_w4_kernel refills (K tile t + 2 loaded into registers while tile t is
-// multiplied, tile t + 1 written from them into the free LDS stage). The 16-row granularity
-// of this MFMA admits tiles the 32 x 32 one does not: 288 x 160 and 256 x 160 cut a 2560-column
-// output at 4352 and 4096 rows into 256 tiles (16 x 16; 192 x 256 tiles leave 26 of 256 CUs
-// idle there), 128 x 160 cuts 4096 x 1280 into 256. A K tile of 64 is two k-steps of 32. In
+// multiplied, tile t + 1 written from them into the free LDS stage); plain, bias, SwiGLU and
+// q|k|v-store epilogues. Besides 256 x 256 and 192 x 256, the 16-row granularity of this MFMA
+// admits tiles the 32 x 32 one does not: 288 x 160 and 256 x 160 cut a 2560-column output at
+// 4352 and 4096 rows into 256 tiles (16 x 16; 192 x 256 tiles leave 26 of 256 CUs idle there),
+// 128 x 160 cuts 4096 x 1280 into 256. A K tile of 64 is two k-steps of 32. In
 // k-step 0 each of the first NR MFMAs is followed by one fragment read of k-step 1, the next
 // ones alternately by an LDS write of the first half of tile t + 1 and the load of tile t + 2
 // into the slot just written. In k-step 1 the second half follows the same way, then the wait
@@ -961,7 +964,8 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   constexpr int A_STAGE = BM * BK, STAGE = (BM + BN) * BK;
   static_assert(WM % 16 == 0 && WN % 16 == 0 && A_LOADS * RPL * NW == BM && B_LOADS * RPL * NW == BN,
                 "tile / wave split");
-  static_assert(EPI == IRIS_EPI_NONE || EPI == IRIS_EPI_SILU_MUL || EPI == kEpiQkRope, "plain, bias, SwiGLU or q|k|v epilogue");
+  static_assert(EPI == IRIS_EPI_NONE || EPI == IRIS_EPI_SILU_MUL || EPI == kEpiQkRope,
+                "plain, bias, SwiGLU or q|k|v epilogue");
   constexpr int W0 = (LW + 1) / 2;             // slots written to LDS (and reloaded) in k-step 0
   constexpr int W1 = LW - W0;                  // the rest, in k-step 1 before its barrier
   static_assert(NR + 2 * W0 <= NM && 2 * W1 + NR < NM && W1 > 0, "MFMAs per k-step");
@@ -1012,7 +1016,8 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   auto load1 = [&](int kt, int i) {
     const int op = i < A_LOADS ? 0 : 1;
     const int j = op ? i - A_LOADS : i;
-    const unsigned soff = static_cast<unsigned>(kt * BK * 2) + static_cast<unsigned>((j & ~1) * RPL) * (op ? ldb2 : lda2);
+    const unsigned soff =
+        static_cast<unsigned>(kt * BK * 2) + static_cast<unsigned>((j & ~1) * RPL) * (op ? ldb2 : lda2);
     staged[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(op ? rsrc_b : rsrc_a, voff[op][j & 1],
                                                                                 static_cast<int>(soff), 0));
   };
