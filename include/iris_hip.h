@@ -174,10 +174,12 @@ int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int
 
 /* Tuning hook for the benchmark sweep and the tile tests: force the GEMM tile of later
  * iris_gemm_bf16* calls made by the calling thread (an index into the tile table of gemm.hip:
- * 0-10 tiles of 256x256, 256x192, 192x256 and 128x128 for the kernel with direct-to-LDS
- * refills; 11 and 12 the four-wave kernel with register-staged refills at 256x256 and 192x256,
- * the automatic choice for most shapes) or restore the automatic choice (-1).
- * The setting is per thread. No counterpart in the reference. */
+ * 0-10 tiles of 256x256, 256x192, 192x256 and 128x128 for the eight-wave 32x32x16-MFMA kernel
+ * with direct-to-LDS refills, the SiLU epilogue's; 11 and 12 the four-wave 32x32x16 kernel at
+ * 256x256 and 192x256; 13-17 the four-wave 16x16x32 kernel at 288x160, 256x160, 128x160,
+ * 256x256 and 192x256, the automatic choice for plain, bias and SwiGLU outputs) or restore the
+ * automatic choice (-1). A forced tile of the other MFMA shape rounds differently from the
+ * automatic one. The setting is per thread. No counterpart in the reference. */
 int iris_gemm_force_tile(int tile);
 
 /* Up to two GEMMs of equal n, k and strides in one launch (the image and text streams of a
