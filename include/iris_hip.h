@@ -197,11 +197,14 @@ int iris_gemm_bf16_grouped(int groups, const void* const* a, const void* const* 
  * (same results) to q BF16 [batch, heads, n_dst, 128] and k_out BF16 [batch, kv_heads, n_dst, 128],
  * row m of group g being token t = m % rows_per_batch[g] of batch item m / rows_per_batch[g], at
  * row dst_offset[g] + t with gains q_weight[g] / k_weight[g] and (cos, sin)[dst_offset[g] + t]
- * (FP32 [table_rows, 64]). The remaining columns (the V heads) go to c (BF16, row stride ldc), whose
- * Q and K columns are not written; or, with vt non-null, transposed to vt as iris_v_heads_t writes
- * them (BF16 [batch, kv_heads, 128, n_vt], n_vt % 64 == 0; same results), which needs every group's
- * rows_per_batch % 256 == 0 and dst_offset % 16 == 0, and then c is not written at all.
- * n % 128 == 0; operands below 2 GiB as for iris_gemm_bf16. */
+ * (FP32 [table_rows, 64]). The remaining columns go to c (BF16, row stride ldc) as iris_gemm_bf16
+ * writes them, and c's Q and K columns are not written; with vt non-null, the kv_heads V heads
+ * after the K heads go instead transposed to vt as iris_v_heads_t writes them (BF16 [batch,
+ * kv_heads, 128, n_vt], n_vt % 64 == 0; same results), which needs n >= (heads + 2 kv_heads) 128,
+ * every group's rows_per_batch % 256 == 0 and dst_offset % 16 == 0, and c then receives only the
+ * columns after the V heads. Columns after the V heads (the attention gate of a q | k | v | gate
+ * weight, src/iris_metal/model.py:282-283, 309) run as a plain product beside the store, in the
+ * same launch for the step's shapes. n % 128 == 0; operands below 2 GiB as for iris_gemm_bf16. */
 int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const void* const* b, void* const* c, const int* m,
                            int n, int k, long lda, long ldb, long ldc, const float* const* q_weight,
                            const float* const* k_weight, const int* rows_per_batch, const int* dst_offset,

@@ -11,7 +11,9 @@
 // - gemm_w4h_kernel (the default for plain, bias and SwiGLU outputs and the q|k|v store): four
 //   waves, one per SIMD, in a 2 x 2 grid of v_mfma_f32_16x16x32_bf16 blocks; K tiles staged
 //   through registers (16-byte buffer loads two K tiles ahead) into a 2-stage LDS ring;
-//   288 x 160, 256 x 160, 128 x 160, 256 x 256 and 192 x 256 tiles.
+//   288 x 160, 256 x 160, 128 x 160, 256 x 256 and 192 x 256 tiles. gemm_w4h_pair_kernel runs
+//   two of its GEMMs in one grid (SwiGLU's two column parts; the q|k|v store and the gate
+//   columns beside it), which saves the boundary between two launches.
 // - gemm_w4_kernel: the same design on v_mfma_f32_32x32x16_bf16 (256 x 256, 192 x 256),
 //   forced-only (a tuning and test reference).
 // - gemm_kernel: eight waves, K tiles global -> LDS with buffer_load_dwordx4 ... lds into a ring
@@ -129,14 +131,16 @@ __device__ __forceinline__ TileJob locate_tile(const GemmArgs& p) {
   return locate_tile_at<BM, BN>(p, xcd_remap(blockIdx.x, p.total_tiles));
 }
 
-// Persistent workgroups: round r of a grid of G workgroups covers logical tiles r G .. r G +
-// G - 1, remapped per XCD as a one-round launch would be; -1 when this workgroup has no tile
-// in round r (only in the last one).
-__device__ __forceinline__ int persistent_tile(const GemmArgs& p, int round) {
-  const int G = gridDim.x;
+// Persistent workgroups: round r of G workgroups (wg = 0 .. G - 1) covers logical tiles r G ..
+// r G + G - 1, remapped per XCD as a one-round launch would be; -1 when this workgroup has no
+// tile in round r (only in the last one). Workgroup wg must run on XCD wg % 8.
+__device__ __forceinline__ int persistent_tile(const GemmArgs& p, int round, int wg, int G) {
   const int base = round * G;
   const int count = min(G, p.total_tiles - base);
-  return static_cast<int>(blockIdx.x) < count ? base + xcd_remap(blockIdx.x, count) : -1;
+  return wg < count ? base + xcd_remap(wg, count) : -1;
+}
+__device__ __forceinline__ int persistent_tile(const GemmArgs& p, int round) {
+  return persistent_tile(p, round, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
 }
 
 // kEpiQkRope, while the accumulators are staged: the Q and K gains of this tile's group go to
@@ -951,8 +955,19 @@ __device__ __forceinline__ void mfma16_acc(f32x4& c, const bf16x8& a, const bf16
 // into the slot just written. In k-step 1 the second half follows the same way, then the wait
 // and barrier that publish tile t + 1 and retire stage t % 2, then one read of tile t + 1's
 // first fragments after each MFMA.
+// Bytes of gemm_w4h_tiles' LDS ring: two stages of BM x 64 and BN x 64 operand tiles (the output
+// staging of the store reuses it). The ring is the launch's dynamic LDS, so that a kernel running
+// two tile shapes holds one ring; the compiler also keeps the constant parts of the fragment and
+// refill addresses as instruction offsets there (a static array reached through a pointer or a
+// helper function cost one address register per access, and spills in the 256 x 256 kernels).
+template <int BM, int BN>
+constexpr unsigned w4h_lds_bytes() {
+  return 2u * (BM + BN) * 64u * sizeof(bf16);
+}
+
+// The body of gemm_w4h_kernel for workgroup wg of nwg (wg on XCD wg % 8).
 template <int BM, int BN, int EPI, typename TC, bool PERSIST>
-__global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
+__device__ __forceinline__ void gemm_w4h_tiles(const GemmArgs& p, const int wg, const int nwg) {
   constexpr int BK = 64, NW = 4;
   constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
   constexpr int CPR = BK / 8;
@@ -969,9 +984,10 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   constexpr int W0 = (LW + 1) / 2;             // slots written to LDS (and reloaded) in k-step 0
   constexpr int W1 = LW - W0;                  // the rest, in k-step 1 before its barrier
   static_assert(NR + 2 * W0 <= NM && 2 * W1 + NR < NM && W1 > 0, "MFMAs per k-step");
-  __shared__ __attribute__((aligned(1024))) bf16 lds[2 * STAGE];
+  static_assert(2 * STAGE * sizeof(bf16) == w4h_lds_bytes<BM, BN>(), "LDS ring");
+  extern __shared__ __attribute__((aligned(1024))) bf16 lds[];  // w4h_lds_bytes<BM, BN>() at launch
 
-  int cur_tile = persistent_tile(p, 0);
+  int cur_tile = persistent_tile(p, 0, wg, nwg);
   if (cur_tile < 0) return;
   TileJob job = locate_tile_at<BM, BN>(p, cur_tile);
   const int N = p.n;
@@ -1141,7 +1157,7 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
     }
   }
   wait_vmcnt<0>();  // the repeated loads of the last K tile
-  const int next_tile = PERSIST ? persistent_tile(p, round + 1) : -1;
+  const int next_tile = PERSIST ? persistent_tile(p, round + 1, wg, nwg) : -1;
   const TileJob next = next_tile >= 0 ? locate_tile_at<BM, BN>(p, next_tile) : job;
   store_tile16<BM, BN, WM, WN, FM, FN, NW, 2 * STAGE, EPI, TC>(acc, lds, job, N, p.ldc, wm, wn, p.qk, [&] {
     if (next_tile >= 0) {
@@ -1155,6 +1171,27 @@ __global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
   __syncthreads();  // every wave is done with the staged output before stage 0 is rewritten
   job = next;
   zero_acc();
+  }
+}
+
+template <int BM, int BN, int EPI, typename TC, bool PERSIST>
+__global__ __launch_bounds__(256) void gemm_w4h_kernel(GemmArgs p) {
+  gemm_w4h_tiles<BM, BN, EPI, TC, PERSIST>(p, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+}
+
+// Two independent GEMMs in one grid, one tile per workgroup, BF16 outputs: workgroups
+// [0, p1.total_tiles) run the first, the second starts at the next multiple of 8 (the workgroups
+// between exit at once), so each keeps the XCD mapping of a launch of its own. Against two
+// launches it saves the boundary between them (the first one's last output writes and the
+// second one's first K tiles overlap on the CUs that finish first).
+template <int BM1, int BN1, int EPI1, int BM2, int BN2, int EPI2>
+__global__ __launch_bounds__(256) void gemm_w4h_pair_kernel(GemmArgs p1, GemmArgs p2) {
+  const int wg = static_cast<int>(blockIdx.x);
+  const int second = (p1.total_tiles + 7) & ~7;
+  if (wg < second) {
+    if (wg < p1.total_tiles) gemm_w4h_tiles<BM1, BN1, EPI1, bf16, false>(p1, wg, p1.total_tiles);
+  } else {
+    gemm_w4h_tiles<BM2, BN2, EPI2, bf16, false>(p2, wg - second, p2.total_tiles);
   }
 }
 
@@ -1225,16 +1262,16 @@ int launch_w4h(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
     // one tile per workgroup, as gemm_w4_kernel's SwiGLU form
     if constexpr (BN / 2 % 64 == 0) {
       if (c_dtype == IRIS_BF16)
-        gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, 0, stream>>>(args);
+        gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, bf16, false><<<all, 256, w4h_lds_bytes<BM, BN>(), stream>>>(args);
       else
-        gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, float, false><<<all, 256, 0, stream>>>(args);
+        gemm_w4h_kernel<BM, BN, IRIS_EPI_SILU_MUL, float, false><<<all, 256, w4h_lds_bytes<BM, BN>(), stream>>>(args);
       return check_launch("gemm_bf16");
     }
   }
   if (epilogue == kEpiQkRope) {
     // one tile per workgroup: the next tile's loads in flight would spill the store's registers
     if constexpr (BM == 256 && BN == 256) {
-      gemm_w4h_kernel<BM, BN, kEpiQkRope, bf16, false><<<all, 256, 0, stream>>>(args);
+      gemm_w4h_kernel<BM, BN, kEpiQkRope, bf16, false><<<all, 256, w4h_lds_bytes<BM, BN>(), stream>>>(args);
       return check_launch("gemm_bf16");
     }
   }
@@ -1242,10 +1279,11 @@ int launch_w4h(GemmArgs& args, int c_dtype, int epilogue, hipStream_t stream) {
     return fail(IRIS_E_UNSUPPORTED, "gemm: the %dx%d tile has no such epilogue", BM, BN);
   const int cus = device_cus();
   if (c_dtype == IRIS_BF16)
-    gemm_w4h_kernel<BM, BN, IRIS_EPI_NONE, bf16, true><<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, 0,
-                                                         stream>>>(args);
+    gemm_w4h_kernel<BM, BN, IRIS_EPI_NONE, bf16, true>
+        <<<dim3(args.total_tiles < cus ? args.total_tiles : cus), 256, w4h_lds_bytes<BM, BN>(), stream>>>(args);
   else
-    gemm_w4h_kernel<BM, BN, IRIS_EPI_NONE, float, false><<<dim3(args.total_tiles), 256, 0, stream>>>(args);
+    gemm_w4h_kernel<BM, BN, IRIS_EPI_NONE, float, false>
+        <<<dim3(args.total_tiles), 256, w4h_lds_bytes<BM, BN>(), stream>>>(args);
   return check_launch("gemm_bf16");
 }
 
@@ -1357,12 +1395,13 @@ int pick_tile(const int* m, int groups, int n, int epilogue, int forced, double*
 }
 
 // Column split: when the last round of 256 x 256 tiles would leave many CUs idle, the first n1
-// columns run as whole rounds of 256 x 256 tiles (tile 16) and the rest as a second launch
-// with its own tile choice, e.g. SwiGLU 4352 x 13696: 765 tiles (3 rounds) + 207 tiles of
-// 192 x 256 (one round) instead of 918 tiles in 4 rounds. A second launch is charged a fixed
-// cost (~3 us). Measured in the denoise step (on the 32 x 32 x 16 tiles then): 0.09 ms per step
-// faster (the round model overstates the gain: the tiles of a partly filled last round run
-// faster than those of a full one). n1 = 0: no split.
+// columns run as whole rounds of 256 x 256 tiles (tile 16) and the rest with their own tile
+// choice, e.g. SwiGLU 4352 x 13696: 765 tiles (3 rounds) + 207 tiles of 192 x 256 (one round)
+// instead of 918 tiles in 4 rounds; both parts in one launch of gemm_w4h_pair_kernel where it
+// has the pair of tiles, else two launches. The second part is charged a fixed cost (~3 us, the
+// gap between two launches). Measured in the denoise step (on the 32 x 32 x 16 tiles, two
+// launches then): 0.09 ms per step faster (the round model overstates the gain: the tiles of a
+// partly filled last round run faster than those of a full one). n1 = 0: no split.
 struct SplitPlan {
   int n1 = 0, tile1 = 16, tile2 = 16;
 };
@@ -1391,11 +1430,12 @@ SplitPlan plan_split(const int* m, int groups, int n, int epilogue, int forced) 
 // per thread: a forced tile never changes another thread's launches
 thread_local int g_forced_tile = -1;
 
-// One launch over output columns [0, n) of operands already offset to the part's first column.
-int gemm_part(int groups, const void* const* a, const void* const* b, const float* const* bias, void* const* c,
-              const int* m, int c_dtype, int n, int k, long lda, long ldb, long ldc, int epilogue, int tile,
-              hipStream_t stream, const QkRope* qk = nullptr) {
-  GemmArgs args{};
+// Launch arguments of one GEMM over output columns [0, n) of operands already offset to the
+// part's first column, on tile shape `tile`.
+int make_args(GemmArgs& args, int groups, const void* const* a, const void* const* b, const float* const* bias,
+              void* const* c, const int* m, int n, int k, long lda, long ldb, long ldc, int epilogue, int tile,
+              const QkRope* qk) {
+  args = GemmArgs{};
   if (qk) args.qk = *qk;
   args.ngroups = groups;
   args.n = n;
@@ -1422,8 +1462,43 @@ int gemm_part(int groups, const void* const* a, const void* const* b, const floa
   }
   if (groups == 1) args.g1 = args.g0, args.g1.tile_begin = begin;
   args.total_tiles = begin;
-  if (begin == 0) return IRIS_OK;
   IRIS_REQUIRE(epilogue != IRIS_EPI_SILU_MUL || shape.swiglu(), "gemm: tile %dx%d has no SwiGLU epilogue", bm, bn);
+  return IRIS_OK;
+}
+
+// The (tile, epilogue) pairs gemm_w4h_pair_kernel is instantiated for, BF16 output: SwiGLU's
+// two column parts (256 x 256, then 192 x 256) and the q|k|v store beside the gate columns
+// (256 x 256, then 288 x 160).
+bool has_pair(int tile1, int epi1, int tile2, int epi2) {
+  return (tile1 == 16 && epi1 == IRIS_EPI_SILU_MUL && tile2 == 17 && epi2 == IRIS_EPI_SILU_MUL) ||
+         (tile1 == kQkRopeTile && epi1 == kEpiQkRope && tile2 == 13 && epi2 == IRIS_EPI_NONE);
+}
+
+int launch_pair(const GemmArgs& a1, int epi1, const GemmArgs& a2, hipStream_t stream) {
+  const dim3 grid(((a1.total_tiles + 7) & ~7) + a2.total_tiles);
+  constexpr unsigned lds = w4h_lds_bytes<256, 256>();  // the larger ring of both pairs
+  static_assert(lds >= w4h_lds_bytes<192, 256>() && lds >= w4h_lds_bytes<288, 160>(), "pair ring");
+  if (epi1 == IRIS_EPI_SILU_MUL)
+    gemm_w4h_pair_kernel<256, 256, IRIS_EPI_SILU_MUL, 192, 256, IRIS_EPI_SILU_MUL><<<grid, 256, lds, stream>>>(a1, a2);
+  else
+    gemm_w4h_pair_kernel<256, 256, kEpiQkRope, 288, 160, IRIS_EPI_NONE><<<grid, 256, lds, stream>>>(a1, a2);
+  return check_launch("gemm_bf16 (two GEMMs)");
+}
+
+int launch_args(GemmArgs& args, int c_dtype, int epilogue, int tile, hipStream_t stream);
+
+// One launch over output columns [0, n) of operands already offset to the part's first column.
+int gemm_part(int groups, const void* const* a, const void* const* b, const float* const* bias, void* const* c,
+              const int* m, int c_dtype, int n, int k, long lda, long ldb, long ldc, int epilogue, int tile,
+              hipStream_t stream, const QkRope* qk = nullptr) {
+  GemmArgs args;
+  const int rc = make_args(args, groups, a, b, bias, c, m, n, k, lda, ldb, ldc, epilogue, tile, qk);
+  if (rc != IRIS_OK) return rc;
+  if (args.total_tiles == 0) return IRIS_OK;
+  return launch_args(args, c_dtype, epilogue, tile, stream);
+}
+
+int launch_args(GemmArgs& args, int c_dtype, int epilogue, int tile, hipStream_t stream) {
   static_assert(kNumTiles == 18, "one case per tile shape");
   switch (tile) {
 #define IRIS_TILE_CASE(I) \
@@ -1451,6 +1526,19 @@ int gemm_part(int groups, const void* const* a, const void* const* b, const floa
     default:
       return fail(IRIS_E_INVALID, "gemm: no tile shape %d", tile);
   }
+}
+
+// Two GEMMs, in one launch when has_pair allows it and both have tiles, else one after the
+// other; the results are the same either way (one MFMA family, every tile sums k in order).
+int launch_two(GemmArgs& a1, int tile1, int epi1, GemmArgs& a2, int tile2, int epi2, int c_dtype,
+               hipStream_t stream) {
+  if (c_dtype == IRIS_BF16 && has_pair(tile1, epi1, tile2, epi2) && a1.total_tiles > 0 && a2.total_tiles > 0)
+    return launch_pair(a1, epi1, a2, stream);
+  if (a1.total_tiles > 0) {
+    const int rc = launch_args(a1, c_dtype, epi1, tile1, stream);
+    if (rc != IRIS_OK) return rc;
+  }
+  return a2.total_tiles > 0 ? launch_args(a2, c_dtype, epi2, tile2, stream) : IRIS_OK;
 }
 
 }  // namespace
@@ -1485,9 +1573,10 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
   if (plan.n1 == 0)
     return gemm_part(groups, a, b, bias, c, m, c_dtype, n, k, lda, ldb, ldc, epilogue,
                      pick_tile(m, groups, n, epilogue, g_forced_tile), stream);
-  // two launches over columns [0, n1) and [n1, n): weight rows, bias entries and output columns
-  // of the second start at n1 (n1 / 2 output columns for SwiGLU)
-  const int rc = gemm_part(groups, a, b, bias, c, m, c_dtype, plan.n1, k, lda, ldb, ldc, epilogue, plan.tile1, stream);
+  // columns [0, n1) and [n1, n): weight rows, bias entries and output columns of the second part
+  // start at n1 (n1 / 2 output columns for SwiGLU); one launch for both where a pair kernel exists
+  GemmArgs a1, a2;
+  int rc = make_args(a1, groups, a, b, bias, c, m, plan.n1, k, lda, ldb, ldc, epilogue, plan.tile1, nullptr);
   if (rc != IRIS_OK) return rc;
   const void* b2[2];
   const float* bias2[2];
@@ -1499,8 +1588,10 @@ extern "C" int iris_gemm_bf16_grouped(int groups, const void* const* a, const vo
     bias2[i] = bias && bias[i] ? bias[i] + plan.n1 : nullptr;
     c2[i] = c[i] ? static_cast<char*>(c[i]) + out_col * out_size : nullptr;
   }
-  return gemm_part(groups, a, b2, bias ? bias2 : nullptr, c2, m, c_dtype, n - plan.n1, k, lda, ldb, ldc, epilogue,
-                   plan.tile2, stream);
+  rc = make_args(a2, groups, a, b2, bias ? bias2 : nullptr, c2, m, n - plan.n1, k, lda, ldb, ldc, epilogue, plan.tile2,
+                 nullptr);
+  if (rc != IRIS_OK) return rc;
+  return launch_two(a1, plan.tile1, epilogue, a2, plan.tile2, epilogue, c_dtype, stream);
 }
 
 extern "C" int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const void* const* b, void* const* c,
@@ -1537,11 +1628,11 @@ extern "C" int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const vo
     IRIS_REQUIRE(static_cast<long>(m[i]) * lda < (1L << 30), "gemm_qk_rope: activation above 2 GiB (32-bit byte offsets)");
   }
   IRIS_REQUIRE(static_cast<long>(n) * ldb < (1L << 30), "gemm_qk_rope: weight above 2 GiB (32-bit byte offsets)");
+  const int n_qkv = (heads + 2 * kv_heads) * 128;  // Q, K and V heads; any columns after them are plain
   if (vt) {
-    // every column past the Q / K heads is a V head of vt: exactly kv_heads of them
-    IRIS_REQUIRE(n == (heads + 2 * kv_heads) * 128,
-                 "gemm_qk_rope: with vt, n (%d) must be exactly the %d Q, %d K and %d V heads of 128 columns", n,
-                 heads, kv_heads, kv_heads);
+    // the kv_heads V heads go to vt (and no other column: the plain columns go to c)
+    IRIS_REQUIRE(n >= n_qkv, "gemm_qk_rope: with vt, n (%d) must cover the %d Q, %d K and %d V heads of 128 columns",
+                 n, heads, kv_heads, kv_heads);
     IRIS_REQUIRE(aligned(vt, 16) && n_vt > 0 && n_vt % 64 == 0 && n_vt < (1L << 30),
                  "gemm_qk_rope: vt must be 16-byte aligned with n_vt a positive multiple of 64");
     for (int i = 0; i < groups; ++i)
@@ -1571,7 +1662,23 @@ extern "C" int iris_gemm_bf16_qk_rope(int groups, const void* const* a, const vo
   qk.eps = eps;
   qk.vt = static_cast<bf16*>(vt);
   qk.n_vt = static_cast<int>(n_vt);
-  return gemm_part(groups, a, b, nullptr, c, m, IRIS_BF16, n, k, lda, ldb, ldc, kEpiQkRope, kQkRopeTile, stream, &qk);
+  if (n <= n_qkv)
+    return gemm_part(groups, a, b, nullptr, c, m, IRIS_BF16, n, k, lda, ldb, ldc, kEpiQkRope, kQkRopeTile, stream, &qk);
+  // the columns after the V heads (the gate columns of a q | k | v | gate weight) are a plain
+  // product into c beside the store, in the same launch where a pair kernel exists
+  GemmArgs a1, a2;
+  int rc = make_args(a1, groups, a, b, nullptr, c, m, n_qkv, k, lda, ldb, ldc, kEpiQkRope, kQkRopeTile, &qk);
+  if (rc != IRIS_OK) return rc;
+  const void* b2[2];
+  void* c2[2];
+  for (int i = 0; i < groups; ++i) {
+    b2[i] = b[i] ? static_cast<const bf16*>(b[i]) + static_cast<long>(n_qkv) * ldb : nullptr;
+    c2[i] = c[i] ? static_cast<bf16*>(c[i]) + n_qkv : nullptr;
+  }
+  const int tile2 = pick_tile(m, groups, n - n_qkv, IRIS_EPI_NONE, g_forced_tile);
+  rc = make_args(a2, groups, a, b2, nullptr, c2, m, n - n_qkv, k, lda, ldb, ldc, IRIS_EPI_NONE, tile2, nullptr);
+  if (rc != IRIS_OK) return rc;
+  return launch_two(a1, kQkRopeTile, kEpiQkRope, a2, tile2, IRIS_EPI_NONE, IRIS_BF16, stream);
 }
 
 extern "C" int iris_gemm_bf16(const void* a, const void* b, const float* bias, void* c, int c_dtype, int m, int n,

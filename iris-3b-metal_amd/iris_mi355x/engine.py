@@ -494,21 +494,19 @@ class HipIris:
         if not h_ready:
             K.rms_norm_modulate(X, blk["norm_x1"], xm[0], xm[1], eps, bf16, out=hx.view(B, Lp, D))
             K.rms_norm_modulate(Y, blk["norm_y1"], ym[0], ym[1], eps, bf16, out=hy.view(B, T, D))
-        # q | k | v with the Q / K norm + rotary in the GEMM's store (text rows at positions 0.., image
-        # rows after them), the V heads transposed from its output, then the gate columns
+        # q | k | v | gate in one launch, the Q / K norm + rotary in the store of the q | k | v
+        # columns (text rows at positions 0.., image rows after them), the V heads transposed
+        # there too or from its output, the gate columns a plain product beside them
         rope_c, rope_s = ws["rope"]
         q, k, vt = ws["q"], ws["k"], ws["vt"]
         gate_col = (H + 2 * Hkv) * HEAD_DIM
         fuse_vt = Lp % 256 == 0 and T % 256 == 0  # whole 256-row tiles per item (and T % 16 == 0)
-        K.linear_qk_rope([hx, hy], [blk["qkvg_x"][:gate_col], blk["qkvg_y"][:gate_col]],
-                         [px[:, :gate_col], py[:, :gate_col]], [blk["q_norm_x"], blk["q_norm_y"]],
+        K.linear_qk_rope([hx, hy], [blk["qkvg_x"], blk["qkvg_y"]], [px, py], [blk["q_norm_x"], blk["q_norm_y"]],
                          [blk["k_norm_x"], blk["k_norm_y"]], rope_c, rope_s, eps, H, Hkv, q, k, [Lp, T], [T, 0],
                          vt=vt if fuse_vt else None)
         if not fuse_vt:
             for proj, rows, off in ((py, T, 0), (px, Lp, T)):
                 K.v_heads_t(proj.view(B, rows, qkvg_w), Hkv, vt, (H + Hkv) * HEAD_DIM, off)
-        K.linear_grouped([hx, hy], [blk["qkvg_x"][gate_col:], blk["qkvg_y"][gate_col:]], None,
-                         [px[:, gate_col:], py[:, gate_col:]])
         K.flash_attention(q, k, vt, N, ay, ax, n_split=T, gate0=py[:, gate_col:], gate1=px[:, gate_col:])
         K.linear_grouped([ax, ay], [blk["proj_x_w"], blk["proj_y_w"]], [blk["proj_x_b"], blk["proj_y_b"]], [bx, by])
         K.gated_residual_grouped_([X, Y], [bx.view(B, Lp, D), by.view(B, T, D)],
@@ -545,12 +543,11 @@ class HipIris:
         q, k, vt = ws["q"], ws["k"], ws["vt"]
         gate_col = (H + 2 * Hkv) * HEAD_DIM  # as in _dual_block
         fuse_vt = N % 256 == 0
-        K.linear_qk_rope([h], [blk["qkvg"][:gate_col]], [proj[:, :gate_col]], [blk["q_norm"]], [blk["k_norm"]],
+        K.linear_qk_rope([h], [blk["qkvg"]], [proj], [blk["q_norm"]], [blk["k_norm"]],
                          rope_c, rope_s, eps, H, Hkv, q, k, [N], [0], vt=vt if fuse_vt else None)
         if not fuse_vt:
             K.v_heads_t(proj.view(B, N, qkvg_w), Hkv, vt, (H + Hkv) * HEAD_DIM)
         gate = proj[:, gate_col:]
-        K.linear(h, blk["qkvg"][gate_col:], out=gate)
         if not last:
             R, M, per_batch = tok, rows, N
             attn = ws["attn"][:rows]

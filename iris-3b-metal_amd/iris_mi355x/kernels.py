@@ -428,14 +428,16 @@ def linear_grouped(xs, weights, biases, outs, swiglu: bool = False) -> None:
 def linear_qk_rope(xs, weights, outs, q_weights, k_weights, cos: torch.Tensor, sin: torch.Tensor, eps: float,
                    heads: int, kv_heads: int, q: torch.Tensor, k: torch.Tensor, rows_per_batch, offsets,
                    vt: torch.Tensor | None = None) -> None:
-    """``linear`` of one or two q | k | v projections (one per stream of a dual block, in one
-    launch) whose Q and K heads go to ``q`` / ``k`` normed and rotated exactly as ``qk_norm_rope``
-    writes them; the columns after them (the V heads) go to ``outs``, or with ``vt`` transposed
-    into it exactly as ``v_heads_t`` writes them (then ``outs`` is not written; every
-    ``rows_per_batch`` a multiple of 256 and every offset of 16). Group ``i``'s rows are batch
-    items of ``rows_per_batch[i]`` tokens, written at rows ``offsets[i] + token`` of ``q`` / ``k``
-    (``[B, heads, N, 128]`` / ``[B, kv_heads, N, 128]``, BF16) with gains ``q_weights[i]`` /
-    ``k_weights[i]`` and the rotary tables' rows ``offsets[i] + token``."""
+    """``linear`` of one or two q | k | v (| gate) projections (one per stream of a dual block, in
+    one launch) whose Q and K heads go to ``q`` / ``k`` normed and rotated exactly as
+    ``qk_norm_rope`` writes them; the columns after them go to ``outs`` as ``linear`` writes them,
+    except that with ``vt`` the ``kv_heads`` V heads go transposed into it exactly as ``v_heads_t``
+    writes them (every ``rows_per_batch`` a multiple of 256 and every offset of 16), and ``outs``
+    then receives only the columns after the V heads (the attention gate of a q | k | v | gate
+    weight). Group ``i``'s rows are batch items of ``rows_per_batch[i]`` tokens, written at rows
+    ``offsets[i] + token`` of ``q`` / ``k`` (``[B, heads, N, 128]`` / ``[B, kv_heads, N, 128]``,
+    BF16) with gains ``q_weights[i]`` / ``k_weights[i]`` and the rotary tables' rows
+    ``offsets[i] + token``."""
     groups = len(xs)
     check = _Check("linear_qk_rope", q, k, cos, sin)
     check(groups in (1, 2) and len(weights) == len(outs) == len(q_weights) == len(k_weights) == groups
@@ -471,9 +473,9 @@ def linear_qk_rope(xs, weights, outs, q_weights, k_weights, cos: torch.Tensor, s
               f"vt must be a contiguous BF16 [{q.shape[0]}, {kv_heads}, 128, N] buffer, N % 64 == 0")
         check(all(r % 256 == 0 and o % 16 == 0 for r, o in zip(rows_per_batch, offsets)),
               "the V^T store needs rows_per_batch % 256 == 0 and offsets % 16 == 0")
-        check(n == (heads + 2 * kv_heads) * HEAD_DIM,
-              f"with vt the weight must hold exactly {heads} Q, {kv_heads} K and {kv_heads} V heads "
-              f"({(heads + 2 * kv_heads) * HEAD_DIM} rows), got {n}")
+        check(n >= (heads + 2 * kv_heads) * HEAD_DIM,
+              f"with vt the weight must hold {heads} Q, {kv_heads} K and {kv_heads} V heads "
+              f"(at least {(heads + 2 * kv_heads) * HEAD_DIM} rows), got {n}")
     L.call(
         "iris_gemm_bf16_qk_rope", groups, L.pointer_array([L.ptr(x) for x in x2]),
         L.pointer_array([L.ptr(w) for w in weights]), L.pointer_array([L.ptr(o) for o in o2]),

@@ -158,16 +158,20 @@ def test_qkv_prepare_is_the_three_calls(heads, kv_heads, n_text, n_image):
     assert torch.all(bufs[1][0][:, :, n:] == 3.0) and torch.all(bufs[1][1][:, :, n:] == 3.0)
 
 
+@pytest.mark.parametrize("gate", [False, True])
 @pytest.mark.parametrize("heads,kv_heads,rows,batch,kdim",
                          [(20, 5, (4352,), 1, 2560), (20, 5, (4096, 256), 1, 2560), (3, 1, (400, 112), 2, 192)])
-def test_linear_qk_rope_is_linear_then_qkv_prepare(heads, kv_heads, rows, batch, kdim):
+def test_linear_qk_rope_is_linear_then_qkv_prepare(heads, kv_heads, rows, batch, kdim, gate):
     """The q | k | v GEMM with the Q / K norm + RoPE in its store writes bit for bit what the plain
     GEMM followed by qkv_prepare writes (Q, K, and the V columns of the output): one group (the
     single-stream block, 4352 tokens), two groups with the second's tokens first (a dual block's
     image and text rows), and two batch items per group with tokens not a multiple of the tile.
-    Other q / k rows and the Q / K columns of the output are left as they were."""
+    Other q / k rows and the Q / K columns of the output are left as they were. With a gate tail
+    (a q | k | v | gate weight: the gate columns run beside the store, in the same launch at the
+    step's shapes) the gate columns are bit for bit the plain GEMM's, with and without V^T."""
     g = torch.Generator(device=DEV).manual_seed(31)
-    n = (heads + 2 * kv_heads) * 128
+    n_qkv = (heads + 2 * kv_heads) * 128
+    n = n_qkv + (heads * 128 if gate else 0)
     v_col = (heads + kv_heads) * 128
     tokens = [r // batch for r in rows]
     offsets = [tokens[1], 0] if len(rows) == 2 else [0]
@@ -204,7 +208,9 @@ def test_linear_qk_rope_is_linear_then_qkv_prepare(heads, kv_heads, rows, batch,
         K.linear_qk_rope(xs, ws, outs, qws, kws, cos, sin, 1e-6, heads, kv_heads, q, k, tokens, offsets, vt=vt2)
         torch.cuda.synchronize()
         assert torch.equal(q, q_ref) and torch.equal(k, k_ref) and torch.equal(vt2, vt)
-        assert all(torch.all(out == 5.0) for out in outs)
+        for out, ref in zip(outs, outs_ref):
+            assert torch.all(out[:, :n_qkv] == 5.0)
+            assert torch.equal(out[:, n_qkv:], ref[:, n_qkv:])
 
 
 def test_linear_qk_rope_rejects_bad_layouts():
@@ -219,20 +225,20 @@ def test_linear_qk_rope_rejects_bad_layouts():
         K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [30], [0])
     with pytest.raises(ValueError, match="outside q/k"):
         K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [100], [40])
-    # with vt every column past the Q / K heads is a V head: a q | k | v | gate weight (one head of
-    # each) would write its gate columns past vt's single V head
+    # with vt the weight must hold all kv_heads V heads: one of Q and K heads only (one head of
+    # each) would leave vt's V head unwritten
     x = torch.zeros(256, 128, device=DEV, dtype=torch.bfloat16)
-    w = torch.zeros(4 * 128, 128, device=DEV, dtype=torch.bfloat16)
-    out = torch.zeros(256, 4 * 128, device=DEV, dtype=torch.bfloat16)
+    w = torch.zeros(2 * 128, 128, device=DEV, dtype=torch.bfloat16)
+    out = torch.zeros(256, 2 * 128, device=DEV, dtype=torch.bfloat16)
     cos = torch.zeros(256, 64, device=DEV)
     q = torch.zeros(1, 1, 256, 128, device=DEV, dtype=torch.bfloat16)
     vt = torch.zeros(1, 1, 128, 256, device=DEV, dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="exactly"):
+    with pytest.raises(ValueError, match="V heads"):
         K.linear_qk_rope([x], [w], [out], [gain], [gain], cos, cos, 1e-6, 1, 1, q, q.clone(), [256], [0], vt=vt)
     # the C entry point refuses it on its own (IRIS_E_INVALID), whatever the caller checked
-    with pytest.raises(ValueError, match="exactly"):
+    with pytest.raises(ValueError, match="V heads"):
         _lib.call("iris_gemm_bf16_qk_rope", 1, _lib.pointer_array([x.data_ptr()]), _lib.pointer_array([w.data_ptr()]),
-                  _lib.pointer_array([out.data_ptr()]), _lib.int_array([256]), 4 * 128, 128, 128, 128, 4 * 128,
+                  _lib.pointer_array([out.data_ptr()]), _lib.int_array([256]), 2 * 128, 128, 128, 128, 2 * 128,
                   _lib.pointer_array([gain.data_ptr()]), _lib.pointer_array([gain.data_ptr()]),
                   _lib.int_array([256]), _lib.int_array([0]), cos.data_ptr(), cos.data_ptr(), 256, q.data_ptr(),
                   q.clone().data_ptr(), 1, 1, 256, vt.data_ptr(), 256, 1e-6, _lib.stream())
@@ -472,6 +478,54 @@ def test_gemm_trunk_shapes(shape):
     rows = torch.arange(0, m, 97)
     want = a[rows].float().cpu() @ w.float().cpu().T
     torch.testing.assert_close(out[rows].cpu(), want, rtol=1e-4, atol=2e-4)
+
+
+@pytest.mark.parametrize("rows", [(4352,), (4096, 256), (4096,), (17408,)])
+def test_gemm_swiglu_column_split_in_one_launch(rows):
+    """SwiGLU w1 | w3 at the step's shapes (the single-stream block, a dual block's grouped image +
+    text rows, the last block's image rows, a guided batch of four): the automatic choice runs
+    the first columns on 256 x 256 tiles and the rest on 192 x 256 tiles in one launch. Bit for
+    bit what a single 256 x 256 tile launch over all columns writes (every tile sums k in order),
+    close to an FP32 product on sampled rows, and the same again when replayed from a HIP graph
+    with eager work and synchronisation between the replays."""
+    n, k = 13696, 2560
+    g = torch.Generator(device=DEV).manual_seed(47)
+    xs = [torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16) for m in rows]
+    ws = [(0.02 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16) for _ in rows]
+
+    def run(outs=None):
+        outs = outs or [torch.full((m, n // 2), 7.0, device=DEV, dtype=torch.bfloat16) for m in rows]
+        if len(rows) == 1:
+            K.linear(xs[0], ws[0], out=outs[0], swiglu=True)
+        else:
+            K.linear_grouped(xs, ws, None, outs, swiglu=True)
+        return outs
+
+    got = run()
+    _lib.call("iris_gemm_force_tile", 16)
+    try:
+        whole = run()
+    finally:
+        _lib.call("iris_gemm_force_tile", -1)
+    for o, w, x, m in zip(got, whole, xs, rows):
+        assert torch.equal(o, w)
+        sel = torch.cat([torch.arange(0, m, 211), torch.tensor([m - 1])])
+        a = x[sel].float().cpu() @ ws[0].float().cpu().T if len(rows) == 1 else None
+        if a is not None:  # interleaved 32-column groups: w1 rows 64p..64p+31, w3 rows 64p+32..
+            a = a.view(-1, n // 64, 2, 32)
+            close_bf16(o[sel].view(-1, n // 64, 32), F.silu(a[:, :, 0]) * a[:, :, 1])
+    outs = [torch.empty_like(o) for o in got]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(outs)
+    for _ in range(3):
+        for o in outs:
+            o.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(o, e) for o, e in zip(outs, got))
+        run()  # eager work between the replays
+        torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("tile", [-1, 0, 1, 4, 5, 6, 7, 8, 9, 10, 11, 12, 16, 17])
