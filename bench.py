@@ -424,10 +424,11 @@ def main() -> None:
                 "launches": launches, "avg_launch_us": 1000.0 * ms / max(launches, 1),
                 "flop_per_launch": fl / max(launches, 1)}
 
-    roofline = {"bound": "mfma", "kernel": "gemm_w4h_kernel<256, 256, SwiGLU> + <192, 256, SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
+    roofline = {"bound": "mfma",
+                "kernel": "gemm_w4h_pair_kernel<256, 256, SwiGLU, 192, 256, SwiGLU> (trunk w1/w3, M x 13652 x 2560)",
                 **rate(True), "traffic": profiled_traffic(),
                 "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if TRAFFIC_PROFILE.exists() else None}
-    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4h_kernel incl. the q|k|v store with Q/K norm + RoPE)", **rate(False)}
+    gemm_all = {"kernel": "every GEMM launch of the step (gemm_w4h_kernel / _pair_kernel, incl. the q|k|v store)", **rate(False)}
     att_source = ATTENTION_TRAFFIC_PROFILE.relative_to(ROOT).as_posix() if ATTENTION_TRAFFIC_PROFILE.exists() else None
     attention = {"kernel": "flash_attn_kernel, trunk joint attention (20 query / 5 K/V heads)",
                  **timer.attention_summary(cfg.num_heads),
