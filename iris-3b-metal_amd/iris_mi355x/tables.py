@@ -21,7 +21,7 @@ def rope_2d_angles(head_dim: int, height: int, width: int, theta: float, scale: 
     """Complex ``[H*W, head_dim/2]`` table of src/iris3b/nn/rope.py:19-82 (x, y pairs interleaved)."""
     n_pairs = head_dim // 4
     if not 0 <= frame_pairs < n_pairs:
-        raise ValueError(f"frame_pairs must be in [0, {n_pairs}), got {frame_pairs}")
+        raise ValueError(f"rope: frame_pairs={frame_pairs} is not one of 0..{n_pairs - 1}")
     freqs = 1.0 / theta ** (torch.arange(0, head_dim, 4)[:n_pairs].float() / head_dim)
     freqs = freqs[: n_pairs - frame_pairs]
     if aspect == "square":
@@ -30,7 +30,7 @@ def rope_2d_angles(head_dim: int, height: int, width: int, theta: float, scale: 
         step = scale / max(max(height, width) - 1, 1)
         xs, ys = torch.arange(width).float() * step, torch.arange(height).float() * step
     else:
-        raise ValueError(f"unknown rope aspect mode '{aspect}'")
+        raise ValueError(f"rope: aspect must be 'square' or 'isotropic', got {aspect!r}")
     x_cis = torch.polar(torch.ones(width, freqs.numel()), torch.outer(xs, freqs))
     y_cis = torch.polar(torch.ones(height, freqs.numel()), torch.outer(ys, freqs))
     cis = torch.stack(

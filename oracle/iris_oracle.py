@@ -98,7 +98,7 @@ def rope_2d(
     """Complex ``[height*width, head_dim//2]`` table; (x, y) frequency pairs interleaved."""
     n_pairs = head_dim // 4
     if not 0 <= frame_pairs < n_pairs:
-        raise ValueError(f"frame_pairs must be in [0, {n_pairs}), got {frame_pairs}")
+        raise ValueError(f"rope: frame_pairs={frame_pairs} is not one of 0..{n_pairs - 1}")
     freqs = 1.0 / theta ** (torch.arange(0, head_dim, 4)[:n_pairs].float() / head_dim)
     freqs = freqs[: n_pairs - frame_pairs]
     if aspect == "square":
@@ -107,7 +107,7 @@ def rope_2d(
         step = scale / max(max(height, width) - 1, 1)
         xs, ys = torch.arange(width).float() * step, torch.arange(height).float() * step
     else:
-        raise ValueError(f"unknown rope aspect mode '{aspect}'")
+        raise ValueError(f"rope: aspect must be 'square' or 'isotropic', got {aspect!r}")
     x_ang, y_ang = torch.outer(xs, freqs), torch.outer(ys, freqs)
     x_cis = torch.polar(torch.ones_like(x_ang), x_ang)[None, :, :].expand(height, width, -1)
     y_cis = torch.polar(torch.ones_like(y_ang), y_ang)[:, None, :].expand(height, width, -1)
