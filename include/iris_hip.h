@@ -121,10 +121,13 @@ int iris_flash_attn(const void* q, const void* k, const void* vt, int batch, int
  * 0: 64-key tiles staged through registers, 1: 32-key tiles staged through registers,
  * 2: 64-key tiles in a 2-stage global_load_lds ring, 3: 32-key tiles in a 3-stage ring,
  * 4: 32-key tiles in a 3-stage ring shared by twelve waves, four query heads by three 32-row
- * blocks) or restore the automatic choice (-1: with four or more query heads per K/V head,
- * variant 4 when its grid of batch * kv_heads * ceil(n / 96) workgroups fills at least 80% of
- * its rounds over the CUs, else variant 1; with fewer, variant 2). The setting is per thread.
- * No counterpart in the reference. */
+ * blocks, 5: variant 4 on v_mfma_f32_16x16x32_bf16 instead of v_mfma_f32_32x32x16_bf16) or
+ * restore the automatic choice (-1: with four or more query heads per K/V head, variant 5 when
+ * one batch item's grid of kv_heads * ceil(n / 96) workgroups fills at least 80% of its rounds
+ * over the CUs, else variant 1, so that a row's result never depends on the batch; with fewer,
+ * variant 2). Variants 1, 3 and 4 give the same bits;
+ * variant 5 sums each score's 128 products and each output's keys in other blocks (to FP32
+ * rounding). The setting is per thread. No counterpart in the reference. */
 int iris_flash_attn_force_variant(int variant);
 
 /* The text refiner's masked attention (SelfAttention.forward with attn_mask = mask | eye,

@@ -455,14 +455,275 @@ flash_attn_kernel(AttnArgs p) {  // 32-row waves: two or three waves per SIMD
   }
 }
 
+// Store of two 16-query blocks of a v_mfma_f32_16x16x32 O^T: o[db][qb][e] is dim 16 db + 4 h + e of
+// query q0 + 16 qb + l16; the lane's partial row sum l_lane covers a quarter of the keys.
+__device__ __forceinline__ void store_rows16(const AttnArgs& p, const f32x4 (&o)[8][2], const float (&l_lane)[2],
+                                             int b, int hd, int q0, int l16, int h) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float l = l_lane[qb] + __shfl_xor(l_lane[qb], 16);
+    l += __shfl_xor(l, 32);
+    const float inv = 1.0f / l;
+    const int row = q0 + 16 * qb + l16;
+    if (row >= p.n) continue;
+    const bool first = row < p.n_split;
+    bf16* out = first ? p.out0 : p.out1;
+    const bf16* gate = first ? p.gate0 : p.gate1;
+    const long r = first ? row : row - p.n_split;
+    if (out == nullptr) continue;
+    bf16* orow = out + (b * (first ? p.out_brows0 : p.out_brows1) + r) * p.ld_out + hd * kHd;
+    const bf16* grow = gate ? gate + (b * (first ? p.gate_brows0 : p.gate_brows1) + r) * p.ld_gate + hd * kHd : nullptr;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int d0 = 16 * db + 4 * h;
+      f32x4 v = o[db][qb] * inv;
+      if (grow) {
+        const f32x4 gv = load4(grow + d0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] *= sigmoid(gv[e]);
+      }
+      store4(orow + d0, v);
+    }
+  }
+}
+
+// The trunk kernel (twelve waves sharing a 3-stage ring of 32-key K / V^T tiles, four query heads
+// x three 32-row blocks) on v_mfma_f32_16x16x32_bf16, which costs less power per FLOP than the
+// 32 x 32 x 16 shape (the GPU is power-limited under MFMA load). A wave's 32 queries are two
+// 16-query blocks; lane l (l16 = l % 16, h = l / 16) holds queries 16 qb + l16 and, of each 32-key
+// tile, the keys kappa_kb(4 h + e) of key blocks kb = 0, 1 (e < 4), with kappa_0(r) = r + 8 (r / 8)
+// and kappa_1(r) = kappa_0(r) + 8: the K fragment of block kb reads key rows kappa_kb(0..15), so
+// that the lane's eight keys are exactly the eight V^T positions 8 h .. 8 h + 7 of the V^T layout
+// (the middle two 4-key quads of every 16 swapped) and P^T stays in registers as the B operand of
+// O^T = V^T P^T. K rows are swizzled by swz_k (key % 16, with bit 3 flipped for odd 16-key halves)
+// so that the sixteen rows of one fragment read hit distinct banks. The softmax is the one of
+// flash_attn_kernel (lazy max, FP32 sums in key order), over the four lanes of a query.
+__device__ __forceinline__ int swz_k(int key) { return (key & 15) ^ (((key >> 4) & 1) << 3); }
+
+template <int STAGES>
+__global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void flash_attn16_kernel(AttnArgs p) {
+  constexpr int NW = 12, KVT = 32;
+  constexpr int TILE = KVT * kHd, STAGE = 2 * TILE;
+  constexpr int LOADS = KVT / 16, LPW = 2 * LOADS;
+  constexpr int VCPR = KVT / 8, VRPL = 64 / VCPR;
+  static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
+
+  int wg = xcd_remap(blockIdx.x, p.total_wg);
+  const int qblk = wg % p.n_qblocks;
+  wg /= p.n_qblocks;
+  const int hg = wg % p.n_hgroups;
+  wg /= p.n_hgroups;
+  const int kvh = wg % p.kv_heads;
+  const int b = wg / p.kv_heads;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int h = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int group = p.heads / p.kv_heads;
+  const int hd = kvh * group + hg * p.hpw + (w % p.hpw);
+  const int q0 = qblk * p.rows_per_wg + (w / p.hpw) * 32;
+  const long n_pad = p.n_pad;
+
+  // Q fragments (B operand of S^T = K Q^T): query q0 + 16 qb + l16, dims 32 st + 8 h .. + 8
+  const bf16* qh = p.q + (static_cast<long>(b) * p.heads + hd) * n_pad * kHd;
+  bf16x8 qf[2][4];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const long row = min(static_cast<long>(q0 + 16 * qb + l16), n_pad - 1);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qf[qb][st] = *reinterpret_cast<const bf16x8*>(qh + row * kHd + 32 * st + 8 * h);
+  }
+
+  const bf16* kh = p.k + (static_cast<long>(b) * p.kv_heads + kvh) * n_pad * kHd;
+  const bf16* vh = p.vt + (static_cast<long>(b) * p.kv_heads + kvh) * kHd * n_pad;
+  // fetch offsets as flash_attn_kernel's, with the K rows swizzled by swz_k
+  int k_off[LOADS], v_off[LOADS];
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    const int kr = (w * LOADS + j) * 4 + (lane >> 4);
+    k_off[j] = kr * kHd + 8 * ((lane & 15) ^ swz_k(kr));
+    const int vd = (w * LOADS + j) * VRPL + lane / VCPR;
+    v_off[j] = vd * static_cast<int>(n_pad) + 8 * ((lane % VCPR) ^ swz<VCPR>(vd));
+  }
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
+  auto issue = [&](int t, int stage) {
+    if (w >= 4) return;  // (wave-uniform: the first four waves fetch)
+    bf16* kl = lds + stage * STAGE;
+    bf16* vl = kl + TILE;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      buffer_load_lds16(rk, kl + (w * LOADS + j) * 512, k_off[j] * 2, t * KVT * kHd * 2);
+      buffer_load_lds16(rv, vl + (w * LOADS + j) * 512, v_off[j] * 2, t * KVT * 2);
+    }
+  };
+
+  f32x4 o[8][2];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) o[db][0] = o[db][1] = f32x4{};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+  const float sl2 = p.scale_log2;
+
+  const int n_tiles = (p.n + KVT - 1) / KVT;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < n_tiles) issue(s, s);
+  // per-lane LDS byte offsets: K fragment (kb, st) at k_rd[kb][st] (key row kappa_kb(l16), chunk
+  // 4 st + h), V^T fragment of dim block db at db * 16 * 2 KVT + v_rd (dim row 16 db + l16, chunk h;
+  // the swizzle of a V^T row does not depend on db)
+  int k_rd[2][4], v_rd;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int key = l16 + 8 * (l16 >> 3) + 8 * kb;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) k_rd[kb][st] = 2 * (key * kHd + 8 * ((4 * st + h) ^ swz_k(key)));
+  }
+  v_rd = 2 * (l16 * KVT + 8 * (h ^ swz<VCPR>(l16)));
+
+  auto tile = [&](const int t, auto stage) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage)::value;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) asm volatile("" : "+v"(k_rd[kb][st]));
+    asm volatile("" : "+v"(v_rd));
+    if (t + STAGES - 2 < n_tiles)
+      wait_vmcnt<(STAGES - 2) * LPW>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // tile t visible; stage (t-1) % STAGES no longer read
+    if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, (S + STAGES - 1) % STAGES);
+    const char* kl = reinterpret_cast<const char*>(lds + S * STAGE);
+    const char* vl = reinterpret_cast<const char*>(lds + S * STAGE + TILE);
+
+    // S^T[key kappa_kb(4 h + e), query 16 qb + l16]; K fragments (i = 2 st + kb) in a ring of 4
+    f32x4 s[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s[kb][0] = s[kb][1] = f32x4{};
+    bf16x8 kf[4];
+    auto read_k = [&](int i) { kf[i % 4] = *reinterpret_cast<const bf16x8*>(kl + k_rd[i % 2][i / 2]); };
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) read_k(i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int st = i / 2, kb = i % 2;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+        s[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i % 4], qf[qb][st], s[kb][qb], 0, 0, 0);
+      if (i + 4 < 8) read_k(i + 4);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int kv0 = t * KVT;
+    if (kv0 + KVT > p.n) {  // tail tile: keys >= n do not exist
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * h + e;
+          const int key = kv0 + r + 8 * (r >> 3) + 8 * kb;
+          if (key >= p.n) s[kb][0][e] = s[kb][1][e] = -INFINITY;
+        }
+    }
+
+    // online softmax as in flash_attn_kernel; a query's keys are spread over lanes l16 + 16 h
+    bf16x8 pf[2];
+    auto probs = [&](int qb, float m) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][e], sl2, -m));
+          pf[qb][4 * kb + e] = from_f32<bf16>(x);
+          sum += x;
+        }
+      return sum;
+    };
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float sum = probs(qb, m_run[qb]);
+      const int need = !(sum <= 256.0f);  // also for NaN / inf partial sums (the first tile)
+      if (__any(need)) {                  // wave-uniform branch
+        int raise = need | __shfl_xor(need, 16);  // (every lane takes part in the exchanges)
+        raise |= __shfl_xor(raise, 32);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kb][qb][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = !raise ? m_run[qb] : fmaxf(m_run[qb], mx * sl2);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);  // exactly 1 unless raised
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[db][qb] *= alpha;
+        m_run[qb] = m_new;
+        sum = probs(qb, m_new);
+      }
+      l_run[qb] += sum;
+    }
+
+    // O^T[dim 16 db + 4 h + e, query] += V^T[dims, keys] P^T[keys, query]; V^T fragments in a ring of 4
+    bf16x8 vfr[4];
+    auto read_v = [&](int db) { vfr[db % 4] = *reinterpret_cast<const bf16x8*>(vl + db * 16 * 2 * KVT + v_rd); };
+#pragma unroll
+    for (int db = 0; db < 4; ++db) read_v(db);
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+        o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfr[db % 4], pf[qb], o[db][qb], 0, 0, 0);
+      if (db + 4 < 8) read_v(db + 4);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  };
+  int t0 = 0;
+  for (; t0 + STAGES <= n_tiles; t0 += STAGES)
+    unroll_stages<STAGES>([&](auto stage) {
+      tile(t0 + decltype(stage)::value, stage);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  unroll_stages<STAGES - 1>([&](auto stage) {
+    if (t0 + decltype(stage)::value < n_tiles) tile(t0 + decltype(stage)::value, stage);
+  });
+  store_rows16(p, o, l_run, b, hd, q0, l16, h);
+}
+
 struct Variant {
   int qb, stages, kvt;
   bool staged;
   int nw = 4;
+  bool mfma16 = false;  // flash_attn16_kernel
 };
 // 0: 32 query rows per wave, 64-key tiles staged through registers; 1: the same with 32-key
 // tiles; 2: 64-key tiles, 2-stage ring; 3: 32-key tiles, 3-stage ring; 4: 32-key
-// tiles in a 3-stage ring shared by twelve waves (four query heads x three row blocks).
+// tiles in a 3-stage ring shared by twelve waves (four query heads x three row blocks); 5: variant
+// 4 on v_mfma_f32_16x16x32_bf16 (flash_attn16_kernel).
 // (Measured and dropped: twelve-wave rings of 4 and 6 stages (1-2% slower than 3), eight of the
 // twelve waves fetching instead of four (2% slower), 64-key tiles at twelve waves (spills); an
 // eight-wave ping-pong of MFMA and softmax phases, 1.8x slower at the trunk shape; a
@@ -472,8 +733,8 @@ struct Variant {
 // SIMD, 1.5-1.9x slower as compiled; the same 96-row, one-wave-per-SIMD form written as inline
 // assembly (each MFMA carrying one score's exp / convert / add, P.V accumulators in fixed AGPRs,
 // a 5- to 8-stage ring), bitwise equal to variant 1 and 4-6% slower than variant 4.)
-constexpr Variant kVariants[] = {
-    {1, 2, 64, true}, {1, 2, 32, true}, {1, 2, 64, false}, {1, 3, 32, false}, {1, 3, 32, false, 12}};
+constexpr Variant kVariants[] = {{1, 2, 64, true},  {1, 2, 32, true},      {1, 2, 64, false},
+                                  {1, 3, 32, false}, {1, 3, 32, false, 12}, {1, 3, 32, false, 12, true}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 // per thread: a forced variant never changes another thread's launches
 thread_local int g_attn_variant = -1;
@@ -523,19 +784,22 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
   args.n_split = static_cast<int>(n_split);
   args.hpw = group < 4 ? group : 4;
   // Grouped heads (the trunk's 20 query / 5 K/V heads): twelve-wave workgroups sharing one K/V
-  // ring (one per CU; 230 of them cover a 4352-token sequence) when their rounds over the CUs
-  // are at least 80% full, 9-11% faster than variant 1 there; else 32-key tiles staged through
-  // registers in three 4-wave workgroups per CU (variant 1: 168 VGPRs; small grids spread
-  // over more CUs). One query head per K/V head (the pixel stage): 64-key tiles in a
-  // 2-stage ring. Each measured fastest at its shapes.
+  // ring (one per CU; 230 of them cover a 4352-token sequence) on the 16 x 16 x 32 MFMA when
+  // their rounds over the CUs are at least 80% full (variant 5; the 32 x 32 x 16 form, variant 4,
+  // was 9-11% faster than variant 1 there, and variant 5 took the step 0.15-0.2 ms below variant
+  // 4); else 32-key tiles staged through registers in three 4-wave workgroups per CU (variant 1:
+  // 168 VGPRs; small grids spread over more CUs). One query head per K/V head (the pixel stage):
+  // 64-key tiles in a 2-stage ring. Each measured fastest at its shapes.
+  // The choice depends on one batch item's shape only: variant 5 rounds differently from
+  // variant 1, and a row's result must not depend on the other items of its batch.
   int variant = g_attn_variant;
   if (variant < 0) {
     variant = group >= 4 ? 1 : 2;
     if (group >= 4) {
       const int cus = device_cus();
-      const long wide = static_cast<long>(batch) * kv_heads * (group / 4) * ((n + 95) / 96);
+      const long wide = static_cast<long>(kv_heads) * (group / 4) * ((n + 95) / 96);
       const long rounds = (wide + cus - 1) / cus;
-      if (wide >= 0.8 * rounds * cus) variant = 4;
+      if (wide >= 0.8 * rounds * cus) variant = 5;
     }
   }
   const Variant v = kVariants[variant];
@@ -560,8 +824,11 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
     case 3:
       flash_attn_kernel<1, 3, 32, false><<<grid, 256, 0, stream>>>(args);
       break;
-    default:
+    case 4:
       flash_attn_kernel<1, 3, 32, false, false, 12><<<grid, dim3(768), 0, stream>>>(args);
+      break;
+    default:
+      flash_attn16_kernel<3><<<grid, dim3(768), 0, stream>>>(args);
       break;
   }
   return check_launch("flash_attn");

@@ -566,7 +566,7 @@ def _attn_inputs(b, h, hkv, n, seed):
 
 
 @pytest.mark.parametrize("n", [333, 352])
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
 def test_flash_attention_variants(variant, n):
     b, h, hkv = 1, 8, 2
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 16)
@@ -601,6 +601,22 @@ def test_flash_attention_32_key_variants_agree_bitwise(n):
         assert torch.equal(outs[0], outs[i]), f"variant {(1, 3, 4)[i]} differs from variant 1"
 
 
+@pytest.mark.parametrize("n", [1000, 4352])
+def test_flash_attention_batch_rows_do_not_depend_on_the_batch(n):
+    """20 query / 5 K/V heads: a batch of four gives each item the bits it gets alone (the
+    automatic variant follows one item's shape: at 1000 tokens a batch-sized grid would have
+    chosen the 16 x 16 x 32 form, which rounds differently from the single item's)."""
+    b, h, hkv = 4, 20, 5
+    q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 23)
+    out = torch.zeros(b * n, h * 128, device=DEV, dtype=torch.bfloat16)
+    K.flash_attention(qd, kd, vt, n, None, out, n_split=0)
+    for i in range(b):
+        one = torch.zeros(n, h * 128, device=DEV, dtype=torch.bfloat16)
+        K.flash_attention(qd[i:i + 1].contiguous(), kd[i:i + 1].contiguous(), vt[i:i + 1].contiguous(), n, None, one,
+                          n_split=0)
+        assert torch.equal(one, out[i * n:(i + 1) * n])
+
+
 @pytest.mark.parametrize("b,h,hkv,n", [(1, 2, 1, 52), (2, 4, 1, 200), (1, 8, 2, 130), (1, 2, 2, 300)])
 def test_flash_attention_small(b, h, hkv, n):
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 8)
@@ -610,7 +626,7 @@ def test_flash_attention_small(b, h, hkv, n):
     close_attention(out.view(b, n, -1), want)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
 def test_flash_attention_rows_do_not_depend_on_padding_rows(variant):
     """A query row's output is bit-identical whatever the padding query rows (>= n) hold: the
     lazy max raise is decided per column, not per wave."""
@@ -630,8 +646,10 @@ def test_flash_attention_rows_do_not_depend_on_padding_rows(variant):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
-def test_flash_attention_trunk_shape_with_gate_and_split():
-    """20 query / 5 K/V heads over 256 text + 4096 image tokens, gate fused, rows split."""
+@pytest.mark.parametrize("variant", [-1, 4, 5])
+def test_flash_attention_trunk_shape_with_gate_and_split(variant):
+    """20 query / 5 K/V heads over 256 text + 4096 image tokens, gate fused, rows split; the
+    automatic choice and both twelve-wave forms (32 x 32 x 16 and 16 x 16 x 32 MFMAs)."""
     b, h, hkv, t, l = 1, 20, 5, 256, 4096
     n = t + l
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 9)
@@ -639,7 +657,11 @@ def test_flash_attention_trunk_shape_with_gate_and_split():
     oy = torch.zeros(t, h * 128, device=DEV, dtype=torch.bfloat16)
     ox = torch.zeros(l, h * 128, device=DEV, dtype=torch.bfloat16)
     gd = gate.to(DEV)
-    K.flash_attention(qd, kd, vt, n, oy, ox, n_split=t, gate0=gd[:t], gate1=gd[t:])
+    _lib.call("iris_flash_attn_force_variant", variant)
+    try:
+        K.flash_attention(qd, kd, vt, n, oy, ox, n_split=t, gate0=gd[:t], gate1=gd[t:])
+    finally:
+        _lib.call("iris_flash_attn_force_variant", -1)
     heads = [0, 3, 4, 7, 18, 19]  # both ends of the first, second and last K/V head's group
     got = torch.cat([oy, ox]).float().cpu().view(n, h, 128)
     sel = torch.cat([torch.arange(0, t, 3), torch.arange(t, n, 7)])  # text and image rows
@@ -704,7 +726,7 @@ def _peak_weight(q, k, hh, hkv_per):
 
 
 @pytest.mark.parametrize("mode", LOGIT_MODES)
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
 def test_flash_attention_large_logits(variant, mode):
     """Every variant (64-key register-staged, 32-key register-staged, 64-key ring, 32-key ring,
     twelve-wave ring) against the FP32 oracle on the same BF16 inputs at large logits."""
