@@ -487,25 +487,29 @@ __device__ __forceinline__ void store_rows16(const AttnArgs& p, const f32x4 (&o)
   }
 }
 
-// The trunk kernel (twelve waves sharing a 3-stage ring of 32-key K / V^T tiles, four query heads
-// x three 32-row blocks) on v_mfma_f32_16x16x32_bf16, which costs less power per FLOP than the
-// 32 x 32 x 16 shape (the GPU is power-limited under MFMA load). A wave's 32 queries are two
-// 16-query blocks; lane l (l16 = l % 16, h = l / 16) holds queries 16 qb + l16 and, of each 32-key
-// tile, the keys kappa_kb(4 h + e) of key blocks kb = 0, 1 (e < 4), with kappa_0(r) = r + 8 (r / 8)
-// and kappa_1(r) = kappa_0(r) + 8: the K fragment of block kb reads key rows kappa_kb(0..15), so
-// that the lane's eight keys are exactly the eight V^T positions 8 h .. 8 h + 7 of the V^T layout
-// (the middle two 4-key quads of every 16 swapped) and P^T stays in registers as the B operand of
-// O^T = V^T P^T. K rows are swizzled by swz_k (key % 16, with bit 3 flipped for odd 16-key halves)
-// so that the sixteen rows of one fragment read hit distinct banks. The softmax is the one of
-// flash_attn_kernel (lazy max, FP32 sums in key order), over the four lanes of a query.
+// flash_attn_kernel's ring variants (twelve waves sharing a 3-stage ring of 32-key K / V^T tiles,
+// or four waves with a 2-stage ring of 64-key tiles) on v_mfma_f32_16x16x32_bf16, which costs less
+// power per FLOP than the 32 x 32 x 16 shape (the GPU is power-limited under MFMA load). A wave's
+// 32 queries are two 16-query blocks; lane l (l16 = l % 16, h = l / 16) holds queries 16 qb + l16
+// and, of each 32 keys of a tile, the keys kappa_kb(4 h + e) of key blocks kb = 0, 1 (e < 4), with
+// kappa_0(r) = r + 8 (r / 8) and kappa_1(r) = kappa_0(r) + 8: the K fragment of block kb reads key
+// rows kappa_kb(0..15), so that the lane's eight keys are exactly the eight V^T positions 8 h ..
+// 8 h + 7 of those 32 keys in the V^T layout (the middle two 4-key quads of every 16 swapped) and
+// P^T stays in registers as the B operand of O^T = V^T P^T. K rows are swizzled by swz_k (key % 16,
+// bit 3 flipped for odd 16-key groups) so that the sixteen rows of one fragment read hit distinct
+// banks. The softmax is the one of flash_attn_kernel (lazy max, FP32 sums in key order), over the
+// four lanes of a query.
 __device__ __forceinline__ int swz_k(int key) { return (key & 15) ^ (((key >> 4) & 1) << 3); }
 
-template <int STAGES>
-__global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void flash_attn16_kernel(AttnArgs p) {
-  constexpr int NW = 12, KVT = 32;
+template <int STAGES, int KVT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 12 ? 3 : 2))) void
+flash_attn16_kernel(AttnArgs p) {
+  constexpr int H32 = KVT / 32;  // 32-key halves of a tile
+  constexpr int NKB = 2 * H32;   // 16-key blocks
   constexpr int TILE = KVT * kHd, STAGE = 2 * TILE;
   constexpr int LOADS = KVT / 16, LPW = 2 * LOADS;
   constexpr int VCPR = KVT / 8, VRPL = 64 / VCPR;
+  static_assert((KVT == 32 || KVT == 64) && (NW == 4 || NW == 12), "tile / workgroup shape");
   static_assert(STAGES >= 2 && (STAGES - 2) * LPW < 64, "pipeline depth");
   __shared__ __attribute__((aligned(1024))) bf16 lds[STAGES * STAGE];
 
@@ -553,7 +557,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void f
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc((void*)vh, (short)0, static_cast<int>(n_pad) * kHd * 2, kBufferFlags);
   auto issue = [&](int t, int stage) {
-    if (w >= 4) return;  // (wave-uniform: the first four waves fetch)
+    if (NW != 4 && w >= 4) return;  // (wave-uniform: the first four waves fetch)
     bf16* kl = lds + stage * STAGE;
     bf16* vl = kl + TILE;
 #pragma unroll
@@ -573,25 +577,27 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void f
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < n_tiles) issue(s, s);
-  // per-lane LDS byte offsets: K fragment (kb, st) at k_rd[kb][st] (key row kappa_kb(l16), chunk
-  // 4 st + h), V^T fragment of dim block db at db * 16 * 2 KVT + v_rd (dim row 16 db + l16, chunk h;
-  // the swizzle of a V^T row does not depend on db)
-  int k_rd[2][4], v_rd;
+  // per-lane LDS byte offsets: K fragment (kb, st) at k_rd[kb][st] (key row 32 (kb / 2) +
+  // kappa_{kb % 2}(l16), chunk 4 st + h), V^T fragment of dim block db and half hf at db * 16 * 2 KVT
+  // + v_rd[hf] (dim row 16 db + l16, chunk 4 hf + h; a V^T row's swizzle does not depend on db)
+  int k_rd[NKB][4], v_rd[H32];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int key = l16 + 8 * (l16 >> 3) + 8 * kb;
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int key = 32 * (kb / 2) + l16 + 8 * (l16 >> 3) + 8 * (kb % 2);
 #pragma unroll
     for (int st = 0; st < 4; ++st) k_rd[kb][st] = 2 * (key * kHd + 8 * ((4 * st + h) ^ swz_k(key)));
   }
-  v_rd = 2 * (l16 * KVT + 8 * (h ^ swz<VCPR>(l16)));
+#pragma unroll
+  for (int hf = 0; hf < H32; ++hf) v_rd[hf] = 2 * (l16 * KVT + 8 * ((4 * hf + h) ^ swz<VCPR>(l16)));
 
   auto tile = [&](const int t, auto stage) __attribute__((always_inline)) {
     constexpr int S = decltype(stage)::value;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int st = 0; st < 4; ++st) asm volatile("" : "+v"(k_rd[kb][st]));
-    asm volatile("" : "+v"(v_rd));
+#pragma unroll
+    for (int hf = 0; hf < H32; ++hf) asm volatile("" : "+v"(v_rd[hf]));
     if (t + STAGES - 2 < n_tiles)
       wait_vmcnt<(STAGES - 2) * LPW>();
     else
@@ -601,28 +607,29 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void f
     const char* kl = reinterpret_cast<const char*>(lds + S * STAGE);
     const char* vl = reinterpret_cast<const char*>(lds + S * STAGE + TILE);
 
-    // S^T[key kappa_kb(4 h + e), query 16 qb + l16]; K fragments (i = 2 st + kb) in a ring of 4
-    f32x4 s[2][2];
+    // S^T[key, query 16 qb + l16] per 16-key block; K fragments (i = NKB st + kb) in a ring of 4
+    constexpr int NK = 4 * NKB;
+    f32x4 s[NKB][2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s[kb][0] = s[kb][1] = f32x4{};
+    for (int kb = 0; kb < NKB; ++kb) s[kb][0] = s[kb][1] = f32x4{};
     bf16x8 kf[4];
-    auto read_k = [&](int i) { kf[i % 4] = *reinterpret_cast<const bf16x8*>(kl + k_rd[i % 2][i / 2]); };
+    auto read_k = [&](int i) { kf[i % 4] = *reinterpret_cast<const bf16x8*>(kl + k_rd[i % NKB][i / NKB]); };
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) read_k(i);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int st = i / 2, kb = i % 2;
+    for (int i = 0; i < NK; ++i) {
+      const int st = i / NKB, kb = i % NKB;
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
         s[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i % 4], qf[qb][st], s[kb][qb], 0, 0, 0);
-      if (i + 4 < 8) read_k(i + 4);
+      if (i + 4 < NK) read_k(i + 4);
     }
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i + 4 < NK; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
@@ -634,25 +641,25 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void f
     const int kv0 = t * KVT;
     if (kv0 + KVT > p.n) {  // tail tile: keys >= n do not exist
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * h + e;
-          const int key = kv0 + r + 8 * (r >> 3) + 8 * kb;
+          const int key = kv0 + 32 * (kb / 2) + r + 8 * (r >> 3) + 8 * (kb % 2);
           if (key >= p.n) s[kb][0][e] = s[kb][1][e] = -INFINITY;
         }
     }
 
     // online softmax as in flash_attn_kernel; a query's keys are spread over lanes l16 + 16 h
-    bf16x8 pf[2];
+    bf16x8 pf[H32][2];
     auto probs = [&](int qb, float m) {
       float sum = 0.0f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][e], sl2, -m));
-          pf[qb][4 * kb + e] = from_f32<bf16>(x);
+          pf[kb / 2][qb][4 * (kb % 2) + e] = from_f32<bf16>(x);
           sum += x;
         }
       return sum;
@@ -666,7 +673,7 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void f
         raise |= __shfl_xor(raise, 32);
         float mx = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kb][qb][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -682,21 +689,25 @@ __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3))) void f
       l_run[qb] += sum;
     }
 
-    // O^T[dim 16 db + 4 h + e, query] += V^T[dims, keys] P^T[keys, query]; V^T fragments in a ring of 4
+    // O^T[dim 16 db + 4 h + e, query] += V^T[dims, keys] P^T[keys, query], one 32-key step per
+    // half; V^T fragments (i = 8 hf + db) in a ring of 4
+    constexpr int NV = 8 * H32;
     bf16x8 vfr[4];
-    auto read_v = [&](int db) { vfr[db % 4] = *reinterpret_cast<const bf16x8*>(vl + db * 16 * 2 * KVT + v_rd); };
+    auto read_v = [&](int i) {
+      vfr[i % 4] = *reinterpret_cast<const bf16x8*>(vl + (i % 8) * 16 * 2 * KVT + v_rd[i / 8]);
+    };
 #pragma unroll
-    for (int db = 0; db < 4; ++db) read_v(db);
+    for (int i = 0; i < 4; ++i) read_v(i);
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
+    for (int i = 0; i < NV; ++i) {
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
-        o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfr[db % 4], pf[qb], o[db][qb], 0, 0, 0);
-      if (db + 4 < 8) read_v(db + 4);
+        o[i % 8][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfr[i % 4], pf[i / 8][qb], o[i % 8][qb], 0, 0, 0);
+      if (i + 4 < NV) read_v(i + 4);
     }
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i + 4 < NV; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
@@ -722,8 +733,8 @@ struct Variant {
 };
 // 0: 32 query rows per wave, 64-key tiles staged through registers; 1: the same with 32-key
 // tiles; 2: 64-key tiles, 2-stage ring; 3: 32-key tiles, 3-stage ring; 4: 32-key
-// tiles in a 3-stage ring shared by twelve waves (four query heads x three row blocks); 5: variant
-// 4 on v_mfma_f32_16x16x32_bf16 (flash_attn16_kernel).
+// tiles in a 3-stage ring shared by twelve waves (four query heads x three row blocks); 5, 6:
+// variants 4 and 2 on v_mfma_f32_16x16x32_bf16 (flash_attn16_kernel).
 // (Measured and dropped: twelve-wave rings of 4 and 6 stages (1-2% slower than 3), eight of the
 // twelve waves fetching instead of four (2% slower), 64-key tiles at twelve waves (spills); an
 // eight-wave ping-pong of MFMA and softmax phases, 1.8x slower at the trunk shape; a
@@ -733,8 +744,9 @@ struct Variant {
 // SIMD, 1.5-1.9x slower as compiled; the same 96-row, one-wave-per-SIMD form written as inline
 // assembly (each MFMA carrying one score's exp / convert / add, P.V accumulators in fixed AGPRs,
 // a 5- to 8-stage ring), bitwise equal to variant 1 and 4-6% slower than variant 4.)
-constexpr Variant kVariants[] = {{1, 2, 64, true},  {1, 2, 32, true},      {1, 2, 64, false},
-                                  {1, 3, 32, false}, {1, 3, 32, false, 12}, {1, 3, 32, false, 12, true}};
+constexpr Variant kVariants[] = {{1, 2, 64, true},       {1, 2, 32, true},  {1, 2, 64, false},
+                                  {1, 3, 32, false},      {1, 3, 32, false, 12},
+                                  {1, 3, 32, false, 12, true}, {1, 2, 64, false, 4, true}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 // per thread: a forced variant never changes another thread's launches
 thread_local int g_attn_variant = -1;
@@ -827,8 +839,11 @@ extern "C" int iris_flash_attn(const void* q, const void* k, const void* vt, int
     case 4:
       flash_attn_kernel<1, 3, 32, false, false, 12><<<grid, dim3(768), 0, stream>>>(args);
       break;
+    case 5:
+      flash_attn16_kernel<3, 32, 12><<<grid, dim3(768), 0, stream>>>(args);
+      break;
     default:
-      flash_attn16_kernel<3><<<grid, dim3(768), 0, stream>>>(args);
+      flash_attn16_kernel<2, 64, 4><<<grid, 256, 0, stream>>>(args);
       break;
   }
   return check_launch("flash_attn");

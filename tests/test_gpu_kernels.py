@@ -566,7 +566,7 @@ def _attn_inputs(b, h, hkv, n, seed):
 
 
 @pytest.mark.parametrize("n", [333, 352])
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6])
 def test_flash_attention_variants(variant, n):
     b, h, hkv = 1, 8, 2
     q, k, v, qd, kd, vt = _attn_inputs(b, h, hkv, n, 16)
@@ -626,7 +626,7 @@ def test_flash_attention_small(b, h, hkv, n):
     close_attention(out.view(b, n, -1), want)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6])
 def test_flash_attention_rows_do_not_depend_on_padding_rows(variant):
     """A query row's output is bit-identical whatever the padding query rows (>= n) hold: the
     lazy max raise is decided per column, not per wave."""
@@ -726,7 +726,7 @@ def _peak_weight(q, k, hh, hkv_per):
 
 
 @pytest.mark.parametrize("mode", LOGIT_MODES)
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6])
 def test_flash_attention_large_logits(variant, mode):
     """Every variant (64-key register-staged, 32-key register-staged, 64-key ring, 32-key ring,
     twelve-wave ring) against the FP32 oracle on the same BF16 inputs at large logits."""
