@@ -725,11 +725,10 @@ flash_attn16_kernel(AttnArgs p) {
   store_rows16(p, o, l_run, b, hd, q0, l16, h);
 }
 
-struct Variant {
+struct Variant {  // (the launch switch below picks the kernel of each)
   int qb, stages, kvt;
   bool staged;
   int nw = 4;
-  bool mfma16 = false;  // flash_attn16_kernel
 };
 // 0: 32 query rows per wave, 64-key tiles staged through registers; 1: the same with 32-key
 // tiles; 2: 64-key tiles, 2-stage ring; 3: 32-key tiles, 3-stage ring; 4: 32-key
@@ -744,9 +743,8 @@ struct Variant {
 // SIMD, 1.5-1.9x slower as compiled; the same 96-row, one-wave-per-SIMD form written as inline
 // assembly (each MFMA carrying one score's exp / convert / add, P.V accumulators in fixed AGPRs,
 // a 5- to 8-stage ring), bitwise equal to variant 1 and 4-6% slower than variant 4.)
-constexpr Variant kVariants[] = {{1, 2, 64, true},       {1, 2, 32, true},  {1, 2, 64, false},
-                                  {1, 3, 32, false},      {1, 3, 32, false, 12},
-                                  {1, 3, 32, false, 12, true}, {1, 2, 64, false, 4, true}};
+constexpr Variant kVariants[] = {{1, 2, 64, true},  {1, 2, 32, true},      {1, 2, 64, false},    {1, 3, 32, false},
+                                  {1, 3, 32, false, 12}, {1, 3, 32, false, 12}, {1, 2, 64, false}};
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 // per thread: a forced variant never changes another thread's launches
 thread_local int g_attn_variant = -1;
