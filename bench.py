@@ -82,7 +82,8 @@ def step_flops(cfg, height: int, width: int, n_text: int, batch: int = 1) -> dic
     pp = p * p
     for _ in range(px.depth):
         gemm += lin(L, D, 4 * pp * px.hidden_size) + lin(L, pp * px.hidden_size, px.attn_hidden_size)
-        gemm += lin(L, px.attn_hidden_size, 3 * px.attn_hidden_size) + lin(L, px.attn_hidden_size, px.attn_hidden_size)
+        # q | k | v, then the attention's output projection folded into expand (one GEMM)
+        gemm += lin(L, px.attn_hidden_size, 3 * px.attn_hidden_size)
         gemm += lin(L, px.attn_hidden_size, pp * px.hidden_size)
         attn += 4.0 * L * L * px.attn_hidden_size
     return {"gemm": gemm * batch, "attention": attn * batch, "total": (gemm + attn) * batch}

@@ -188,6 +188,14 @@ class HipIris:
         self.img_bias = torch.stack(img_bias).contiguous()
         self.txt_bias = torch.stack(txt_bias).contiguous()
 
+        def fold(outer: str, inner: str) -> tuple[torch.Tensor, torch.Tensor]:
+            """``outer(inner(x))`` of two Linears as one: W = W_o W_i, b = W_o b_i + b_o, from the
+            BF16 weights the GEMMs would use, in FP32, W rounded to BF16 once."""
+            wo, wi = w(outer).float(), w(inner).float()
+            weight = bf(wo @ wi)
+            bias = (wo @ f32(f"{inner}.bias") + f32(f"{outer}.bias")).contiguous()
+            return weight, bias
+
         self.pix_w, self.pix_b = f32("pixel_embedder.proj.weight"), f32("pixel_embedder.proj.bias")
         self.pixel_blocks = []
         for j in range(cfg.pixel.depth):
@@ -198,8 +206,9 @@ class HipIris:
                 "compress_w": w(f"{b}.compress"), "compress_b": f32(f"{b}.compress.bias"),
                 "qkv_w": w(f"{b}.attn.qkv"),
                 "q_norm": f32(f"{b}.attn.q_norm.weight"), "k_norm": f32(f"{b}.attn.k_norm.weight"),
-                "proj_w": w(f"{b}.attn.proj"), "proj_b": f32(f"{b}.attn.proj.bias"),
-                "expand_w": w(f"{b}.expand"), "expand_b": f32(f"{b}.expand.bias"),
+                # the attention's output projection and the expand Linear back to pixels, with nothing
+                # between them (src/iris_metal/model.py:340-341), folded into one GEMM
+                **dict(zip(("proj_expand_w", "proj_expand_b"), fold(f"{b}.expand", f"{b}.attn.proj"))),
                 "fc1_w": f32(f"{b}.mlp.fc1.weight"), "fc1_b": f32(f"{b}.mlp.fc1.bias"),
                 "fc2_w": f32(f"{b}.mlp.fc2.weight"), "fc2_b": f32(f"{b}.mlp.fc2.bias"),
             })
@@ -296,7 +305,7 @@ class HipIris:
             "pixels": e(B * Lp, pp, K.PIXEL_WIDTH, dtype=f32), "hpix": e(B * Lp, pp, K.PIXEL_WIDTH),
             "mods_pix": e(B * Lp, pp, 4 * K.PIXEL_WIDTH),
             "cp": e(B * Lp, px.attn_hidden_size), "pq": e(B * Lp, 3 * px.attn_hidden_size),
-            "pa": e(B * Lp, px.attn_hidden_size), "pr": e(B * Lp, px.attn_hidden_size),
+            "pa": e(B * Lp, px.attn_hidden_size),
             "ex": e(B * Lp, pp * K.PIXEL_WIDTH),
             "qp": e(B, px.num_heads, l_pad, HEAD_DIM), "kp": e(B, px.num_heads, l_pad, HEAD_DIM),
             "vtp": torch.zeros(B, px.num_heads, HEAD_DIM, l_pad, device=dev, dtype=bf16),
@@ -587,8 +596,7 @@ class HipIris:
         K.qkv_prepare(pv, blk["q_norm"], blk["k_norm"], rope_c, rope_s, eps, heads, heads, ws["qp"], ws["kp"],
                       ws["vtp"], 0, width, 2 * width)
         K.flash_attention(ws["qp"], ws["kp"], ws["vtp"], Lp, None, ws["pa"], n_split=0)
-        K.linear(ws["pa"], blk["proj_w"], blk["proj_b"], out=ws["pr"])
-        K.linear(ws["pr"], blk["expand_w"], blk["expand_b"], out=ws["ex"])
+        K.linear(ws["pa"], blk["proj_expand_w"], blk["proj_expand_b"], out=ws["ex"])
         K.pixel_mlp_(ws["pixels"], ws["ex"].view_as(ws["hpix"]), ws["mods_pix"], blk["norm2"],
                      (blk["fc1_w"], blk["fc1_b"]), (blk["fc2_w"], blk["fc2_b"]), next_norm, eps,
                      next_input=ws["hpix"])

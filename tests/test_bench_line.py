@@ -46,11 +46,12 @@ def test_traffic_summaries_are_read_and_travel():
 
 
 def test_step_flops_of_the_benchmarked_workload():
-    """22.66 TFLOP per 1024x1024 step with 256 text tokens (the figure the line divides by)."""
+    """22.61 TFLOP per 1024x1024 step with 256 text tokens, as the engine computes it (the pixel
+    stage's attention projection folded into expand; the figure the line divides by)."""
     from iris_mi355x.config import IRIS_3B
 
     total = bench.step_flops(IRIS_3B, 1024, 1024, 256)["total"]
-    assert abs(total / 1e12 - 22.66) < 0.01
+    assert abs(total / 1e12 - 22.61) < 0.01
 
 
 def test_more_than_one_gpu_is_refused():
