@@ -13,10 +13,10 @@ accumulation; every activation crossing a GEMM is stored BF16 once.
 Data layout in HBM (per call shape, allocated once and reused):
 - dual-stream phase: image ``X`` ``[B*L, D]`` and text ``Y`` ``[B*T, D]`` FP32 residuals;
 - single-stream phase: ``tok`` ``[B*N, D]`` FP32 with the text rows first in each batch;
-- packed projections ``[rows, 6400]`` = ``q | k | v | gate``: two GEMMs per stream and block, the
-  q | k | v one writing the attention inputs below straight from its store (Q / K normed and
-  rotated; V transposed when each batch item is whole 256-row tiles, else its V columns land
-  here for ``v_heads_t``), the gate one its columns here;
+- packed projections ``[rows, 6400]`` = ``q | k | v | gate``: one call per block over the packed
+  weight (two GEMMs in one launch), the q | k | v one writing the attention inputs below
+  straight from its store (Q / K normed and rotated; V transposed when each batch item is whole
+  256-row tiles, else its V columns land here for ``v_heads_t``), the gate one its columns here;
 - attention inputs ``q`` ``[B, 20, N_pad, 128]``, ``k`` ``[B, 5, N_pad, 128]``, ``v^T`` ``[B, 5, 128, N_pad]``;
 - pixel stream ``[B*L, p*p, 16]`` FP32 and its BF16 normed copy, adaLN mods ``[B*L, p*p, 64]`` BF16.
 """
