@@ -12,7 +12,8 @@ accumulation; every activation crossing a GEMM is stored BF16 once.
 
 Data layout in HBM (per call shape, allocated once and reused):
 - dual-stream phase: image ``X`` ``[B*L, D]`` and text ``Y`` ``[B*T, D]`` FP32 residuals;
-- single-stream phase: ``tok`` ``[B*N, D]`` FP32 with the text rows first in each batch;
+- single-stream phase: ``tok`` ``[B*N, D]`` FP32 with the text rows first in each batch (for one
+  batch item ``Y`` and ``X`` are its first ``T`` and last ``L`` rows, so the join copies nothing);
 - packed projections ``[rows, 6400]`` = ``q | k | v | gate``: one call per block over the packed
   weight (two GEMMs in one launch), the q | k | v one writing the attention inputs below
   straight from its store (Q / K normed and rotated; V transposed when each batch item is whole
@@ -310,6 +311,11 @@ class HipIris:
             "qp": e(B, px.num_heads, l_pad, HEAD_DIM), "kp": e(B, px.num_heads, l_pad, HEAD_DIM),
             "vtp": torch.zeros(B, px.num_heads, HEAD_DIM, l_pad, device=dev, dtype=bf16),
         }
+        # one batch item: the dual-stream residuals are the single-stream buffer's text and image
+        # rows, so joining the streams (and the last block's image rows) moves nothing
+        ws["joined_in_place"] = B == 1
+        if B == 1:
+            ws["Y"], ws["X"] = ws["tok"][:T], ws["tok"][T:]
         # text-stream scratch of the dual blocks lives after the image rows of the shared buffers
         key = ((hp, wp), T)
         if key not in self._tables:
@@ -404,8 +410,9 @@ class HipIris:
                 h_ready = fuse
                 continue
             if not joined:
-                K.copy_rows(Y, ws["tok"], B, T, 0, T, 0, N)
-                K.copy_rows(ws["X"], ws["tok"], B, Lp, 0, Lp, T, N)
+                if not ws["joined_in_place"]:
+                    K.copy_rows(Y, ws["tok"], B, T, 0, T, 0, N)
+                    K.copy_rows(ws["X"], ws["tok"], B, Lp, 0, Lp, T, N)
                 joined = True
             self._single_block(ws, blk, B, T, Lp, N, i == cfg.depth - 1, h_ready, nxt)
             h_ready = nxt is not None
@@ -564,7 +571,8 @@ class HipIris:
         else:
             # the text rows still feed attention but no output depends on them (model.py:307-308)
             R, M, per_batch = ws["X"], B * Lp, Lp
-            K.copy_rows(tok, R, B, Lp, T, N, 0, Lp)
+            if not ws["joined_in_place"]:
+                K.copy_rows(tok, R, B, Lp, T, N, 0, Lp)
             attn = ws["attn"][:M]
             K.flash_attention(q, k, vt, N, None, attn, n_split=T, gate1=gate[T:],
                               out_batch_rows=(T, Lp), gate_batch_rows=(T, N))
