@@ -32,6 +32,8 @@ Prints one JSON line. Besides the driver's fields it carries:
   algorithmic TFLOP over its HIP-event time against the BF16 peak;
 - ``guided``: 20 first-order guided steps (scale 3.0) over two prompts, a batch of four
   forwards per step (conditional N(0,1) tokens, zero unconditional tokens);
+- ``pcie_inclusive``: the forward with the image and text tokens in pinned host memory, copied in
+  and the velocity copied out around each call (never ``value``, which starts in HBM);
 - ``encode_text``: the once-per-prompt text adapter (12 encoder layers of 2560 per token,
   300 tokens of which 200 are real, batch 1) on the GPU, and the FP32 CPU oracle of the same
   prompt beside it (unless ``--no-cpu-baseline``).
@@ -327,6 +329,32 @@ def guided_leg(engine, cfg, dev, size: int, n_text: int) -> dict:
             "step_tflop": step_tflop, "mfma_frac": step_tflop * 20 / total / BF16_PEAK_TFLOPS}
 
 
+def host_buffer_leg(engine, noise, text, t, reps: int = 20) -> dict:
+    """The forward with the caller's tensors in host memory: the image and text tokens copied in
+    and the velocity copied out over PCIe (pinned buffers) around each call. Not the headline
+    value, which starts from inputs resident in HBM (as the reference's engine takes tensors that
+    are already on its device)."""
+    import torch
+
+    dev = noise.device
+    x_h, text_h = noise.cpu().pin_memory(), text.cpu().pin_memory()
+    v_h = torch.empty_like(x_h).pin_memory()
+
+    def call():
+        v = engine(x_h.to(dev, non_blocking=True), t, text_h.to(dev, non_blocking=True))
+        v_h.copy_(v, non_blocking=True)
+
+    call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        call()
+    torch.cuda.synchronize()
+    ms = 1000.0 * (time.perf_counter() - t0) / reps
+    return {"ms_per_forward": ms, "forwards_per_s": 1000.0 / ms, "reps": reps,
+            "bytes_in": x_h.numel() * 4 + text_h.numel() * 4, "bytes_out": v_h.numel() * 4}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -461,6 +489,8 @@ def main() -> None:
         extras["single_block"] = single_block_leg(engine, cfg, text, dev)
         say("guided sampling, 20 steps, batch 4")
         extras["guided"] = guided_leg(engine, cfg, dev, size, n_text)
+        say("forward with host-resident inputs and output (PCIe-inclusive)")
+        extras["pcie_inclusive"] = host_buffer_leg(engine, noise, text, times[0])
 
     # the once-per-prompt text adapter
     states, mask = text_prompt(cfg)
