@@ -265,6 +265,30 @@ def copy(gib: float, iters: int = 5) -> dict:
     return {"kernel": "copy", "bytes": nbytes, "us": ms * 1e3, "GB/s": nbytes / (ms * 1e-3) / 1e9}
 
 
+def qkvg(n: int = 4352, iters: int = 20, rotate: int = 6) -> dict:
+    """A single-stream block's packed q | k | v | gate projection as the step runs it
+    (``K.linear_qk_rope``: the Q / K norm + RoPE and the V^T layout in the q | k | v store, the gate
+    columns beside it in the same launch) over ``n`` tokens of one batch item (a multiple of 256),
+    each call on the next of ``rotate`` weight copies so that every call reads its weight from HBM."""
+    heads, kv_heads, d = 20, 5, 2560
+    cols = (2 * heads + 2 * kv_heads) * 128
+    n_pad = (n + 63) // 64 * 64
+    bf16 = torch.bfloat16
+    h = (0.5 * torch.randn(n, d, device="cuda")).to(bf16)
+    ws = [(0.02 * torch.randn(cols, d, device="cuda")).to(bf16) for _ in range(rotate)]
+    qw, kw = 1 + 0.1 * torch.randn(128, device="cuda"), 1 + 0.1 * torch.randn(128, device="cuda")
+    cos, sin = torch.randn(n_pad, 64, device="cuda"), torch.randn(n_pad, 64, device="cuda")
+    q = torch.empty(1, heads, n_pad, 128, device="cuda", dtype=bf16)
+    k = torch.empty(1, kv_heads, n_pad, 128, device="cuda", dtype=bf16)
+    vt = torch.zeros(1, kv_heads, 128, n_pad, device="cuda", dtype=bf16)
+    out = torch.empty(n, cols, device="cuda", dtype=bf16)
+    ms = _time(lambda i: K.linear_qk_rope([h], [ws[i % rotate]], [out], [qw], [kw], cos, sin, 1e-6, heads, kv_heads,
+                                          q, k, [n], [0], vt=vt), iters)
+    tflops = 2.0 * n * cols * d / (ms * 1e-3) / 1e12
+    return {"kernel": "gemm_bf16_qk_rope (q|k|v|gate)", "n": n, "cols": cols, "k": d, "us": ms * 1e3,
+            "TFLOP/s": tflops, "mfma_frac": tflops / MFMA_TFLOPS}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -281,6 +305,8 @@ def main() -> None:
     for name in ("b", "h", "hkv", "n"):
         p.add_argument(name, type=int)
     p.add_argument("--variant", type=int, default=-1)
+    p = sub.add_parser("qkvg")
+    p.add_argument("n", type=int, nargs="?", default=4352)
     p = sub.add_parser("pixel-mlp")
     p.add_argument("pixels", type=int, nargs="?", default=1 << 20)
     p = sub.add_parser("copy")
@@ -299,6 +325,8 @@ def main() -> None:
         out = out[0] if len(out) == 1 else out
     elif args.cmd == "attention":
         out = attention(args.b, args.h, args.hkv, args.n, variant=args.variant)
+    elif args.cmd == "qkvg":
+        out = qkvg(args.n)
     elif args.cmd == "pixel-mlp":
         out = pixel_mlp(args.pixels)
     elif args.cmd == "encode-text":
